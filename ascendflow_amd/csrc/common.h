@@ -1,0 +1,72 @@
+// Shared device helpers for the gfx950 attention kernels: b16 vector types,
+// MFMA wrappers, LDS address-space casts and the XCD-aware block remap.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace afa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define AFA_LDS __attribute__((address_space(3)))
+
+// Storage type tags. DT_BF16 and DT_F16 are the values of the C-ABI `dtype`.
+enum { DT_BF16 = 0, DT_F16 = 1 };
+
+template <int DT> struct B16;
+template <> struct B16<DT_BF16> {
+  typedef __bf16 scalar;
+  typedef bf16x8 x8;
+  typedef bf16x4 x4;
+  static __device__ __forceinline__ f32x4 mfma(x8 a, x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ x4 read_tr(const AFA_LDS void* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((x4 AFA_LDS*)p);
+  }
+};
+template <> struct B16<DT_F16> {
+  typedef _Float16 scalar;
+  typedef f16x8 x8;
+  typedef f16x4 x4;
+  static __device__ __forceinline__ f32x4 mfma(x8 a, x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ x4 read_tr(const AFA_LDS void* p) {
+    typedef __fp16 fp16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+    return __builtin_bit_cast(x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 AFA_LDS*)p));
+  }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Wave-wide reductions over the four lanes {l, l^16, l^32, l^48} that hold the
+// same MFMA output column.
+__device__ __forceinline__ float max_over_lane_groups(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float sum_over_lane_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Blocks are dispatched round-robin over the 8 XCDs of an MI355X. Map the
+// hardware block id to a logical id so that each XCD receives a contiguous
+// range of logical ids (neighbouring work shares that XCD's L2).
+__device__ __forceinline__ uint32_t xcd_contiguous(uint32_t b, uint32_t n) {
+  const uint32_t x = b & 7u, local = b >> 3;
+  const uint32_t per = n >> 3, extra = n & 7u;
+  return x * per + (x < extra ? x : extra) + local;
+}
+
+}  // namespace afa

@@ -1,0 +1,6 @@
+"""Sparse MLA (examples/sparse_attention in the reference) on MI355X."""
+
+from .attention import sparse_mla
+from .gather import sparse_mla_gather
+
+__all__ = ["sparse_mla", "sparse_mla_gather"]

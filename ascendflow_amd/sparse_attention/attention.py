@@ -1,0 +1,167 @@
+"""TND sparse shared-KV attention (DeepSeek V4.1 sparse MLA) on MI355X.
+
+Drop-in for ``examples/sparse_attention/attention.py:210-246`` (``sparse_mla``):
+same tensor arguments in the same order, same constexpr keywords and defaults.
+The call launches the fused gfx950 kernel of ``csrc/sparse_mla.hip`` through
+the C ABI ``launch_sparse_mla`` on the current PyTorch-ROCm stream and returns
+without synchronising, as the reference launcher does
+(``docs/guide/runtime.md:86-89``).
+
+Tiling constexprs that only describe the Ascend pipeline (ROWS, GROUPS, VR, BK,
+C, PARTS) are accepted and checked against the reference's own asserts
+(``attention.py:253-262``) so that the same calls are valid or rejected, but
+they do not change the gfx950 schedule.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+
+import torch
+
+from .. import _native
+from .._tensors import DTYPES, check_disjoint, check_tensor, require, storage_dtype, stream_handle
+
+
+def check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PARTS, GROUPS, VR, BK, C, SCALE):
+    """The reference's specialisation asserts (``attention.py:253-262``)."""
+    require(0 < B < 2**31 and 0 < T < 2**31, "nonempty INT32 TND prefix")
+    require(H % BM == 0 and BM in (32, 64), "complete head tiles")
+    require(WINDOW == 128 and PAGE == 128 and BK == 512 and C == 128, "cache/tile geometry")
+    require(D % C == 0 and S == WINDOW + -(-TOPK // BK) * BK, "complete selected capacities")
+    require(PARTS == 1 and ROWS in (16, 32) and GROUPS > 0, "sparse query policy")
+    require(VR in (4, 8, 16) and (BM // 2) % VR == 0, "softmax row groups")
+    require(RATIO in (1, 2) and MAX_SEQ % PAGE == 0, "complete C1/C2 pages")
+    require(-(-S // 512) * 512 <= 4096, "resident softmax capacity")
+    require(SCALE > 0.0, "positive attention scale")
+    require(D in (128, 256, 512), "gfx950 kernel supports D in {128, 256, 512}")
+
+
+def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows=None):
+    return _native.SparseMlaParams(
+        B=B,
+        T=T,
+        H=H,
+        D=D,
+        PAGE=PAGE,
+        RATIO=RATIO,
+        MAX_SEQ=MAX_SEQ,
+        ORI_BLOCKS=ORI_BLOCKS,
+        CMP_BLOCKS=CMP_BLOCKS,
+        WINDOW=WINDOW,
+        TOPK=TOPK,
+        S=S,
+        BM=BM,
+        dtype=_native.AFA_DTYPE[dtype],
+        scale=SCALE,
+        reserved=0,
+        debug_rows=None if debug_rows is None else debug_rows.data_ptr(),
+    )
+
+
+def check_inputs(tensors, *, B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, TOPK, dtype, out_name="attention_out"):
+    """Shape/dtype/device/contiguity contract of ``attention.py:211-224``."""
+    b16 = DTYPES[dtype]
+    i32 = torch.int32
+    width = MAX_SEQ // PAGE
+    shapes = {
+        "q": ((T, H, D), b16),
+        "ori_kv": ((ORI_BLOCKS, PAGE, 1, D), b16),
+        "cmp_kv": ((CMP_BLOCKS, PAGE // RATIO, 1, D), b16),
+        "cmp_sparse_indices": ((T, 1, TOPK), i32),
+        "ori_block_table": ((B, width), i32),
+        "cmp_block_table": ((B, width), i32),
+        "cu_seqlens_q": ((B + 1,), i32),
+        "seqused_ori_kv": ((B,), i32),
+        "seqused_cmp_kv": ((B,), i32),
+        "cmp_residual_kv": ((B,), i32),
+        "ori_topk_length": ((T, 1), i32),
+        "sinks": ((H,), torch.float32),
+        out_name: ((T, H, D), b16),
+    }
+    device = None
+    for name, tensor in tensors.items():
+        shape, dt = shapes[name]
+        check_tensor(name, tensor, shape, dt, device)
+        device = tensor.device
+    check_disjoint([(name, t, name == out_name) for name, t in tensors.items()])
+    return device
+
+
+def sparse_mla(
+    q,
+    ori_kv,
+    cmp_kv,
+    cmp_sparse_indices,
+    ori_block_table,
+    cmp_block_table,
+    cu_seqlens_q,
+    seqused_ori_kv,
+    seqused_cmp_kv,
+    cmp_residual_kv,
+    ori_topk_length,
+    sinks,
+    attention_out,
+    B=4,
+    T=16,
+    H=64,
+    D=512,
+    PAGE=128,
+    RATIO=2,
+    MAX_SEQ=4096,
+    ORI_BLOCKS=128,
+    CMP_BLOCKS=128,
+    WINDOW=128,
+    TOPK=512,
+    ROWS=32,
+    S=640,
+    BM=64,
+    PARTS=1,
+    GROUPS=20,
+    VR=16,
+    BK=512,
+    C=128,
+    DTYPE="bf16",
+    SCALE=0.04419417382415922,
+    *,
+    debug_rows=None,
+):
+    """Sparse MLA forward; writes ``attention_out`` [T, H, D] and returns it.
+
+    ``debug_rows`` (optional int32 [T, S, 2] device tensor) receives the
+    kernel's own row selection per gather slot: (cache, physical row),
+    cache 0 = ori_kv, 1 = cmp_kv, (-1, -1) unused.
+    """
+    dtype = storage_dtype(DTYPE)
+    check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PARTS, GROUPS, VR, BK, C, SCALE)
+    tensors = {
+        "q": q,
+        "ori_kv": ori_kv,
+        "cmp_kv": cmp_kv,
+        "cmp_sparse_indices": cmp_sparse_indices,
+        "ori_block_table": ori_block_table,
+        "cmp_block_table": cmp_block_table,
+        "cu_seqlens_q": cu_seqlens_q,
+        "seqused_ori_kv": seqused_ori_kv,
+        "seqused_cmp_kv": seqused_cmp_kv,
+        "cmp_residual_kv": cmp_residual_kv,
+        "ori_topk_length": ori_topk_length,
+        "sinks": sinks,
+        "attention_out": attention_out,
+    }
+    device = check_inputs(
+        tensors, B=B, T=T, H=H, D=D, PAGE=PAGE, RATIO=RATIO, MAX_SEQ=MAX_SEQ,
+        ORI_BLOCKS=ORI_BLOCKS, CMP_BLOCKS=CMP_BLOCKS, TOPK=TOPK, dtype=dtype,
+    )
+    if debug_rows is not None:
+        check_tensor("debug_rows", debug_rows, (T, S, 2), torch.int32, device)
+    params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows)
+    lib = _native.library()
+    status = lib.launch_sparse_mla(
+        stream_handle(device),
+        *(tensors[name].data_ptr() for name in tensors),
+        None,
+        ct.byref(params),
+    )
+    _native.check(status, "launch_sparse_mla")
+    return attention_out

@@ -1,0 +1,237 @@
+"""Sparse-MLA benchmark on one MI355X (the reference's headline table, README.md:22-39).
+
+A "step" is one sparse_mla launch over the whole configuration, preceded
+(untimed) by a cache-eviction sweep, as the reference evicts L2 before every
+launch and reports the device-task duration (README.md:56-57). Kernel time is
+taken with HIP events on the launch stream around the launch alone; the
+median over the K timed steps is reported.
+
+Headline (``value``): sparse-MLA prefill, Q 8192 tokens over a 32K context
+in effective TFLOPS = 4*H*D*sum(valid rows) / kernel
+time (README.md:38). The decode configuration (B64 x 6 queries over 128K,
+configs[3]) and the 32K prefill are reported alongside in
+``extra``, each with ms, TFLOPS and its roofline fraction.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+FLUSH_BYTES = 1 << 30       # > 4x the 256 MiB Infinity Cache
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def time_launches(launch, steps, warmup, flush):
+    import torch
+
+    for _ in range(warmup):
+        flush()
+        launch()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    times = []
+    wall0 = time.perf_counter()
+    for _ in range(steps):
+        flush()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        launch()
+        end.record(stream)
+        times.append((start, end))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = [s.elapsed_time(e) for s, e in times]
+    return statistics.median(ms), ms, wall
+
+
+def sparse_config(name, batch, queries, context, steps, warmup, flush, device):
+    import torch
+
+    from ascendflow_amd.sparse_attention import sparse_mla
+    from ascendflow_amd.sparse_attention.inputs import compulsory_bytes, effective_flops, make_inputs, measurement_policy
+
+    t0 = time.perf_counter()
+    policy = measurement_policy(batch=batch, query_tokens=queries, context=context)
+    inputs = make_inputs(policy, context, device=device)
+    torch.cuda.synchronize()
+    log(f"[bench] {name}: inputs ready in {time.perf_counter() - t0:.1f}s")
+    args, kwargs = inputs.call_args(), inputs.call_kwargs()
+    median, samples, wall = time_launches(lambda: sparse_mla(*args, **kwargs), steps, warmup, flush)
+    flops = effective_flops(policy, inputs.host, context)
+    nbytes = compulsory_bytes(policy, inputs.touched)
+    tflops = flops / (median * 1e-3) / 1e12
+    gbs = nbytes / (median * 1e-3) / 1e9
+    log(f"[bench] {name}: median {median:.4f} ms, {tflops:.1f} TFLOPS, {gbs:.0f} GB/s")
+    return {
+        "workload": name,
+        "B": batch,
+        "T": policy["T"],
+        "context": context,
+        "ms": round(median, 5),
+        "ms_min": round(min(samples), 5),
+        "ms_max": round(max(samples), 5),
+        "tflops": round(tflops, 2),
+        "flops": flops,
+        "compulsory_bytes": nbytes,
+        "gbs": round(gbs, 1),
+        "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "wall_s": round(wall, 3),
+        "_inputs": inputs,
+    }
+
+
+def cpu_baseline(result, sample_tokens):
+    """Time the oracle's vectorised FP32 PyTorch-CPU sparse MLA on a token sample."""
+    import numpy as np
+    import torch
+
+    from oracle.cpu_reference import CpuSparseMla
+    from tests.sparse_helpers import host_view
+
+    inputs = result["_inputs"]
+    policy = inputs.policy
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(0)
+    tokens = sorted(rng.choice(policy["T"], min(sample_tokens, policy["T"]), replace=False).tolist())
+    data = host_view(inputs, tokens)
+    q_rows = np.stack([data["q"][t] for t in tokens])
+    ref = CpuSparseMla(data, policy, q_rows, tokens)
+    ref.run()  # warm
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ref.run()
+        runs.append(time.perf_counter() - t0)
+    seconds = statistics.median(runs)
+    fraction = len(tokens) / policy["T"]
+    flops = result["flops"] * fraction
+    cpu_model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(flops / seconds / 1e12, 4),
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(tokens)} of {policy['T']} tokens of {result['workload']}; median of 3 runs "
+                  f"{seconds:.3f} s (scaled full config {seconds / fraction * 1e3:.1f} ms); "
+                  f"FP32 torch CPU, {cpu_model}",
+        "ms_full_scaled": round(seconds / fraction * 1e3, 2),
+    }
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k"], default=None,
+                        help="time one configuration only (profiling runs)")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-sample", type=int, default=1024, help="tokens in the CPU-baseline sample")
+    parser.add_argument("--no-flush", action="store_true", help="keep caches warm between launches")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the sparse-MLA path shards by query token with no exchange; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from ascendflow_amd import _native
+
+    device = torch.device("cuda:0")
+    lib = _native.library()
+    flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device=device)
+    stream = lambda: torch.cuda.current_stream(device).cuda_stream
+
+    def flush():
+        if not args.no_flush:
+            _native.check(lib.launch_cache_flush(stream(), flush_buf.data_ptr(), FLUSH_BYTES), "cache flush")
+
+    configs = {
+        "prefill8k": ("sparse_mla prefill B1 Q8192 ctx32768", 1, 8192, 32768),
+        "decode": ("sparse_mla decode B64x6 ctx131072", 64, 6, 131072),
+        "prefill32k": ("sparse_mla prefill B1 Q32768 ctx32768", 1, 32768, 32768),
+    }
+    order = [args.only] if args.only else ["prefill8k", "decode", "prefill32k"]
+    results = {}
+    for key in order:
+        name, b, q, ctx = configs[key]
+        results[key] = sparse_config(name, b, q, ctx, args.steps, args.warmup, flush, device)
+        if key != order[0]:
+            results[key].pop("_inputs")  # free device memory of secondary configs
+            torch.cuda.empty_cache()
+
+    head_key = order[0]
+    head = results[head_key]
+    baseline = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing CPU baseline")
+        baseline = cpu_baseline(head, args.cpu_sample)
+    head.pop("_inputs", None)
+
+    bound = "hbm" if head_key == "decode" else "mfma"
+    achieved = head["gbs"] if bound == "hbm" else head["tflops"]
+    peak = HBM_PEAK_GBS if bound == "hbm" else MFMA_PEAK_TFLOPS
+    record = {
+        "metric": "sparse-MLA kernel ms + TFLOPS (prefill Q8K/32K; decode B64x6 @128K), 1 GPU",
+        "value": head["tflops"],
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.1 Q/KV, sorted top-k without replacement, zero caches with touched rows patched)",
+        "config": {
+            "workload": head["workload"],
+            "H": 64, "kv_heads": 1, "D": 512, "window": 128, "topk": 512, "ratio": 2, "page": 128,
+            "T": head["T"], "context": head["context"], "B": head["B"],
+            "timing": "HIP events around each launch, cache-eviction sweep before each, median",
+        },
+        "roofline": {
+            "bound": bound,
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": {k: v for k, v in baseline.items() if k != "ms_full_scaled"} if baseline else None,
+        "extra": {k: {kk: vv for kk, vv in v.items() if kk != "_inputs"} for k, v in results.items()},
+        "reference_ascend_910b3_ms": {"prefill8k": 6.847, "prefill32k": 27.225, "decode": 0.410},
+    }
+    if baseline:
+        record["extra"]["cpu_ms_full_scaled"] = baseline["ms_full_scaled"]
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,141 @@
+/*
+ * ascendflow_amd C ABI: MI355X (gfx950) sparse-MLA and flash-attention launchers.
+ *
+ * Drop-in counterparts of the launchers the reference's back end emits for its
+ * three attention operators (src/backend/structured.py:573-649):
+ *   int launch_<k>(void* stream, void* arg_<tensor>..., [void* workspace], [int64 sizes]);
+ *   int kernel_config_<k>(int64_t cfg[5]);
+ *   const char* kernel_metadata_<k>(void);
+ *   int workspace_size_<k>(uint64_t* bytes, ...);   (src/backend/workspace.py:100-130)
+ *
+ * The reference specialises every size as a DSL constexpr; here the sizes are
+ * runtime fields of a small parameter struct passed by pointer, because the
+ * drop-in surface is the Python entry signature, not the Ascend binary.
+ *
+ * Conventions (all entry points):
+ *  - every tensor argument is a device pointer to contiguous row-major memory;
+ *    the caller allocates all tensors, outputs included, and keeps them
+ *    pairwise disjoint (docs/guide/runtime.md:86-89 in the reference);
+ *  - launches are asynchronous on `stream` (a hipStream_t, NULL = default);
+ *  - return value: 0 on success, a negative AFA_E* code for a rejected
+ *    configuration, or a positive hipError_t if the launch itself failed.
+ *    Nothing is retried (src/runtime/kernel.py:59-63).
+ */
+#ifndef ASCENDFLOW_AMD_H
+#define ASCENDFLOW_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  AFA_OK = 0,
+  AFA_E_NULL = -1,        /* a required pointer is NULL */
+  AFA_E_SHAPE = -2,       /* unsupported or inconsistent size */
+  AFA_E_DTYPE = -3,       /* unsupported storage dtype */
+  AFA_E_WORKSPACE = -4,   /* workspace missing or too small */
+};
+
+enum { AFA_DTYPE_BF16 = 0, AFA_DTYPE_F16 = 1 };
+
+/* Sizes and policy of one sparse_mla call
+ * (examples/sparse_attention/attention.py:225-245). */
+typedef struct SparseMlaParams {
+  int32_t B, T, H, D;
+  int32_t PAGE, RATIO, MAX_SEQ;
+  int32_t ORI_BLOCKS, CMP_BLOCKS;
+  int32_t WINDOW, TOPK, S, BM;
+  int32_t dtype;            /* AFA_DTYPE_* of q, caches and attention_out */
+  float scale;              /* SCALE, > 0 */
+  int32_t reserved;
+  /* Optional debug image of the row selection, NULL normally: int32 [T, S, 2]
+   * holding (cache, physical_row) per gather slot, cache 0 = ori_kv,
+   * 1 = cmp_kv, (-1, -1) for an unused slot.  Written by the fused kernel
+   * itself, from the same row list it then attends over. */
+  int32_t* debug_rows;
+} SparseMlaParams;
+
+/* Sparse MLA forward: examples/sparse_attention/attention.py:210-525.
+ * Tensor order is the reference entry order (attention.py:211-224):
+ *   q [T,H,D], ori_kv [ORI_BLOCKS,PAGE,1,D], cmp_kv [CMP_BLOCKS,PAGE/RATIO,1,D],
+ *   cmp_sparse_indices i32 [T,1,TOPK], ori_block_table i32 [B,MAX_SEQ/PAGE],
+ *   cmp_block_table i32 [B,MAX_SEQ/PAGE], cu_seqlens_q i32 [B+1],
+ *   seqused_ori_kv i32 [B], seqused_cmp_kv i32 [B], cmp_residual_kv i32 [B],
+ *   ori_topk_length i32 [T,1], sinks f32 [H], attention_out [T,H,D] (written).
+ * `workspace` may be NULL: the fused kernel needs none (workspace_size = 0). */
+int launch_sparse_mla(void* stream, const void* q, const void* ori_kv, const void* cmp_kv,
+                      const int32_t* cmp_sparse_indices, const int32_t* ori_block_table,
+                      const int32_t* cmp_block_table, const int32_t* cu_seqlens_q,
+                      const int32_t* seqused_ori_kv, const int32_t* seqused_cmp_kv,
+                      const int32_t* cmp_residual_kv, const int32_t* ori_topk_length,
+                      const float* sinks, void* attention_out, void* workspace,
+                      const SparseMlaParams* params);
+
+/* Gather image of the sparse selection, the layout of the reference's gather
+ * workspace and of its gather oracle (benchmarks/attention/sparse_reference.py:174-181,
+ * examples/sparse_attention/gather.py:86-131, window slots from gather.py:38-60):
+ *   kv_out [T,S,D] (dtype of the caches; unused slots zero),
+ *   bias_out f32 [T,S] (0 selected, -inf unused).
+ * Uses the fused kernel's own slot resolution and row copy. */
+int launch_sparse_mla_gather(void* stream, const void* ori_kv, const void* cmp_kv,
+                             const int32_t* cmp_sparse_indices, const int32_t* ori_block_table,
+                             const int32_t* cmp_block_table, const int32_t* cu_seqlens_q,
+                             const int32_t* seqused_ori_kv, const int32_t* seqused_cmp_kv,
+                             const int32_t* cmp_residual_kv, const int32_t* ori_topk_length,
+                             void* kv_out, float* bias_out, const SparseMlaParams* params);
+
+/* Flash attention (BNSD): examples/flash_attention/attention.py:243-417.
+ *   Q [B,HQ,Sq,D], K/V [B,HKV,Sk,D], O [B,HQ,Sq,D] (written).
+ * The reference launcher is (stream, Q, K, V, O, workspace, Sq, Sk). */
+typedef struct FaParams {
+  int32_t B, HQ, HKV, D;
+  int32_t dtype;   /* AFA_DTYPE_* */
+  int32_t causal;  /* top-left j <= i masking (attention.py:96-110) */
+  float scale;
+  int32_t reserved;
+} FaParams;
+
+int launch_attention_target(void* stream, const void* Q, const void* K, const void* V, void* O,
+                            void* workspace, int64_t Sq, int64_t Sk, const FaParams* params);
+
+/* Teaching attention: examples/flash_attention/simple.py:60-141.
+ *   Q [H,S,128] f16, K/V [H,128,128] f16, O [H,S,128] f16 (written);
+ * softmax(QK^T / sqrt(128)) normalised before the f16 cast of P. */
+int launch_simple_attention(void* stream, const void* Q, const void* K, const void* V, void* O,
+                            void* workspace, int64_t S, int64_t H);
+
+/* kernel_config_<k>: cfg[5] = {tensors, runtime parameters, has_workspace,
+ * compute units, SIMDs per CU} (src/backend/structured.py:619-637). */
+int kernel_config_sparse_mla(int64_t cfg[5]);
+int kernel_config_attention_target(int64_t cfg[5]);
+int kernel_config_simple_attention(int64_t cfg[5]);
+
+/* kernel_metadata_<k>: versioned JSON naming tensors, dtypes, shapes and
+ * access modes (src/backend/abi.py:19-59). Static storage. */
+const char* kernel_metadata_sparse_mla(void);
+const char* kernel_metadata_attention_target(void);
+const char* kernel_metadata_simple_attention(void);
+
+/* workspace_size_<k>: bytes of the optional workspace (0 for all three fused
+ * kernels); returns -1 on a NULL output pointer (src/backend/workspace.py:100-130). */
+int workspace_size_sparse_mla(uint64_t* bytes, const SparseMlaParams* params);
+int workspace_size_attention_target(uint64_t* bytes, int64_t Sq, int64_t Sk,
+                                    const FaParams* params);
+int workspace_size_simple_attention(uint64_t* bytes, int64_t S, int64_t H);
+
+/* Measurement helpers (no reference kernel; the reference sweeps a >= 4x L2
+ * buffer before each timed launch, benchmarks/cache.py:13-92 and
+ * benchmarks/cache_sweep.py:15-32). Streams `bytes` of `buffer` through the
+ * caches with a read-modify-write so the next launch starts cold. */
+int launch_cache_flush(void* stream, void* buffer, uint64_t bytes);
+
+/* Library version string. */
+const char* ascendflow_amd_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASCENDFLOW_AMD_H */

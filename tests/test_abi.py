@@ -1,0 +1,118 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared symbol, and its
+host-side queries and argument rejections work without touching a GPU."""
+
+import ctypes as ct
+import json
+import re
+from pathlib import Path
+
+import pytest
+
+from ascendflow_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "ascendflow_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _native.library()
+
+
+def test_header_declares_exactly_the_bound_symbols():
+    assert declared_functions() == sorted(_native.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_kernel_config_and_workspace_queries(lib):
+    for kernel, tensors in (("sparse_mla", 13), ("attention_target", 4), ("simple_attention", 4)):
+        cfg = (ct.c_int64 * 5)()
+        assert getattr(lib, f"kernel_config_{kernel}")(cfg) == 0
+        assert cfg[0] == tensors and cfg[2] == 0 and cfg[3] == 256 and cfg[4] == 4
+        meta = json.loads(getattr(lib, f"kernel_metadata_{kernel}")().decode())
+        assert meta["kernel"] == kernel and len(meta["tensors"]) == tensors
+        assert meta["disjoint_external"] is True
+    size = ct.c_uint64(123)
+    assert lib.workspace_size_sparse_mla(ct.byref(size), None) == 0 and size.value == 0
+    assert lib.workspace_size_sparse_mla(None, None) == -1
+    assert lib.workspace_size_attention_target(ct.byref(size), 8, 8, None) == 0 and size.value == 0
+    assert lib.workspace_size_simple_attention(None, 64, 1) == -1
+    assert b"gfx950" in lib.ascendflow_amd_version()
+
+
+def test_sparse_metadata_lists_tensors_in_reference_order(lib):
+    from oracle.sparse_reference import TENSOR_ORDER
+
+    meta = json.loads(lib.kernel_metadata_sparse_mla().decode())
+    assert tuple(t["name"] for t in meta["tensors"]) == TENSOR_ORDER
+    assert [t["access"] for t in meta["tensors"]].count("write") == 1
+
+
+def good_params(**overrides):
+    fields = dict(B=4, T=16, H=64, D=512, PAGE=128, RATIO=2, MAX_SEQ=4096, ORI_BLOCKS=128, CMP_BLOCKS=128,
+                  WINDOW=128, TOPK=512, S=640, BM=64, dtype=0, scale=0.044, reserved=0, debug_rows=None)
+    fields.update(overrides)
+    return _native.SparseMlaParams(**fields)
+
+
+@pytest.mark.parametrize(
+    "overrides,status",
+    [
+        ({"D": 384}, -2),
+        ({"BM": 16}, -2),
+        ({"H": 96}, -2),
+        ({"RATIO": 3}, -2),
+        ({"S": 100}, -2),
+        ({"scale": 0.0}, -2),
+        ({"dtype": 7}, -3),
+        ({"ORI_BLOCKS": 1 << 24}, -2),
+    ],
+)
+def test_sparse_launcher_rejects_bad_configurations_before_any_launch(lib, overrides, status):
+    params = good_params(**overrides)
+    args = [None] + [ct.c_void_p(16)] * 13 + [None]
+    assert lib.launch_sparse_mla(*args, ct.byref(params)) == status
+
+
+def test_launchers_reject_null_arguments(lib):
+    params = good_params()
+    assert lib.launch_sparse_mla(*([None] * 15), None) == -1
+    assert lib.launch_sparse_mla(*([None] * 15), ct.byref(params)) == -1
+    assert lib.launch_sparse_mla_gather(*([None] * 13), ct.byref(params)) == -1
+    fa = _native.FaParams(B=1, HQ=8, HKV=8, D=128, dtype=1, causal=0, scale=0.088, reserved=0)
+    assert lib.launch_attention_target(None, None, None, None, None, None, 8, 8, ct.byref(fa)) == -1
+    p = ct.c_void_p(16)
+    assert lib.launch_attention_target(None, p, p, p, p, None, 0, 8, ct.byref(fa)) == -2
+    fa.HKV = 3
+    assert lib.launch_attention_target(None, p, p, p, p, None, 8, 8, ct.byref(fa)) == -2
+    assert lib.launch_simple_attention(None, p, p, p, p, None, 100, 1) == -2
+    assert lib.launch_cache_flush(None, None, 1024) == -1
+
+
+def test_python_entries_check_the_reference_asserts_before_launching():
+    from ascendflow_amd.sparse_attention.attention import check_policy
+
+    good = dict(B=4, T=16, H=64, D=512, PAGE=128, RATIO=2, MAX_SEQ=4096, WINDOW=128, TOPK=512, ROWS=32, S=640,
+                BM=64, PARTS=1, GROUPS=20, VR=16, BK=512, C=128, SCALE=0.044)
+    check_policy(**good)
+    for bad in ({"WINDOW": 64}, {"S": 512}, {"BM": 48}, {"VR": 3}, {"RATIO": 4}, {"SCALE": -1.0}, {"PARTS": 2}):
+        with pytest.raises(ValueError):
+            check_policy(**dict(good, **bad))
+    from ascendflow_amd.flash_attention import causal_policy
+
+    assert causal_policy(1000, 9000) == {"kv_tile": 256, "vector_rows": 16}
+    assert causal_policy(4096, 4096) == {"kv_tile": 512, "vector_rows": 16}
+    assert causal_policy(8192, 8192) == {"kv_tile": 1024, "vector_rows": 8}
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _native.library(tmp_path / "absent.so")

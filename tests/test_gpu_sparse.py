@@ -1,0 +1,123 @@
+"""GPU parity of the fused sparse-MLA kernel against the CPU oracle.
+
+Row selection is checked bit-exactly through the kernel's own debug image of
+its row list and through the gather-image kernel; outputs against the FP32
+oracle under the tolerance contract (max|err| <= 1e-2 * max|ref|, plus the
+reference runner's rtol 0.02 / atol 0.005). Every case also checks the 512
+guard bytes after the output and that no input changed
+(benchmarks/attention/run_sparse.py:241-262 does the same on Ascend).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sparse_reference as sr
+from tests.sparse_helpers import (INT_KEYS, assert_close, call_args, call_kwargs, expected_rows, guard_intact, host_view,
+                                  to_device)
+
+pytestmark = pytest.mark.gpu
+
+VARIANTS = {
+    "bf16-d512-bm64-r2": dict(DTYPE="bf16", D=512, H=64, BM=64, RATIO=2),
+    "bf16-d512-bm32-r2": dict(DTYPE="bf16", D=512, H=64, BM=32, RATIO=2),
+    "f16-d256-bm64-r1": dict(DTYPE="f16", D=256, H=64, BM=64, RATIO=1),
+    "bf16-d128-bm32-r2": dict(DTYPE="bf16", D=128, H=32, BM=32, RATIO=2),
+}
+
+
+def run_case(policy, data, device):
+    from ascendflow_amd.sparse_attention import sparse_mla, sparse_mla_gather
+
+    tensors = to_device(data, policy, device)
+    before = {k: tensors[k].clone() for k in sr.TENSOR_ORDER if k != "attention_out"}
+    debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug)
+    kv, bias = sparse_mla_gather(*(tensors[k] for k in ("ori_kv", "cmp_kv", *INT_KEYS)),
+                                 **{k: policy[k] for k in ("B", "T", "D", "PAGE", "RATIO", "MAX_SEQ", "ORI_BLOCKS",
+                                                           "CMP_BLOCKS", "WINDOW", "TOPK", "S", "DTYPE")})
+    torch.cuda.synchronize()
+    assert guard_intact(tensors), "kernel wrote past attention_out"
+    for k, v in before.items():
+        assert torch.equal(tensors[k], v), f"input {k} changed"
+    return tensors, debug.cpu().numpy(), kv.float().cpu().numpy(), bias.cpu().numpy()
+
+
+@pytest.mark.parametrize("variant", list(VARIANTS))
+@pytest.mark.parametrize("case", sr.CASES)
+def test_validation_cases_match_oracle(device, case, variant):
+    print(f"\n[sparse] case={case} variant={variant}", flush=True)
+    policy = sr.default_policy(B=4, T=16, MAX_SEQ=4096, ORI_BLOCKS=64, CMP_BLOCKS=64, **VARIANTS[variant])
+    policy["SCALE"] = policy["D"] ** -0.5
+    data = sr.inputs(policy, case)
+    tensors, debug, kv, bias = run_case(policy, data, device)
+    tokens = list(range(policy["T"]))
+    np.testing.assert_array_equal(debug, expected_rows(data, policy, tokens))
+    kv_ref, bias_ref = sr.gather_oracle(data, policy)
+    np.testing.assert_array_equal(bias, bias_ref)
+    np.testing.assert_array_equal(kv, kv_ref)
+    actual = tensors["attention_out"].float().cpu().numpy()
+    assert_close(actual, sr.oracle_fp32(data, policy), policy["DTYPE"])
+    if case == "empty":
+        assert np.all(actual == 0)
+
+
+def test_relaunch_is_bitwise_deterministic(device):
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    policy = sr.default_policy(B=4, T=16, MAX_SEQ=4096, ORI_BLOCKS=64, CMP_BLOCKS=64)
+    data = sr.inputs(policy, "mixed")
+    tensors = to_device(data, policy, device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy))
+    first = tensors["attention_out"].clone()
+    for _ in range(3):
+        sparse_mla(*call_args(tensors), **call_kwargs(policy))
+    torch.cuda.synchronize()
+    assert torch.equal(first, tensors["attention_out"])
+
+
+def check_measured(inputs, tokens, device):
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    policy = inputs.policy
+    debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
+    sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), debug_rows=debug)
+    torch.cuda.synchronize()
+    data = host_view(inputs, tokens)
+    index = torch.as_tensor(tokens, device=device)
+    np.testing.assert_array_equal(debug[index].cpu().numpy(), expected_rows(data, policy, tokens))
+    actual = inputs.tensors["attention_out"][index].float().cpu().numpy()
+    return assert_close(actual, sr.oracle_fp32(data, policy, tokens), policy["DTYPE"])
+
+
+def test_decode_b64x6_ctx128k_all_tokens(device):
+    """Decode configuration: every one of the 384 tokens."""
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+
+    print("\n[sparse] decode B64x6 ctx 131072", flush=True)
+    policy = measurement_policy(batch=64, query_tokens=6, context=131072)
+    inputs = make_inputs(policy, 131072, device=device)
+    check_measured(inputs, list(range(policy["T"])), device)
+
+
+def test_prefill_q8k_ctx32k_sampled_tokens(device):
+    """Prefill configuration on a spread sample of tokens."""
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+
+    print("\n[sparse] prefill T8192 ctx 32768", flush=True)
+    policy = measurement_policy(batch=1, query_tokens=8192, context=32768)
+    inputs = make_inputs(policy, 32768, device=device)
+    rng = np.random.default_rng(5)
+    tokens = sorted({0, 1, 31, 32, 8191, *rng.choice(8192, 90, replace=False).tolist()})
+    check_measured(inputs, tokens, device)
+
+
+def test_prefill_from_empty_cache_has_growing_selections(device):
+    """Q = context: early tokens have short windows and few compressed rows."""
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+
+    print("\n[sparse] prefill T4096 ctx 4096", flush=True)
+    policy = measurement_policy(batch=1, query_tokens=4096, context=4096)
+    inputs = make_inputs(policy, 4096, device=device)
+    tokens = list(range(0, 40)) + list(range(100, 4096, 97)) + [4095]
+    check_measured(inputs, tokens, device)
