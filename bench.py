@@ -152,6 +152,8 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-sample", type=int, default=1024, help="tokens in the CPU-baseline sample")
     parser.add_argument("--no-flush", action="store_true", help="keep caches warm between launches")
+    parser.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                        help="also run a plain device copy of MIB MiB (PMC byte-counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -170,6 +172,15 @@ def main():
     def flush():
         if not args.no_flush:
             _native.check(lib.launch_cache_flush(stream(), flush_buf.data_ptr(), FLUSH_BYTES), "cache flush")
+
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration << 18, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 3 copies of {args.copy_calibration} MiB")
+        del src, dst
 
     configs = {
         "prefill8k": ("sparse_mla prefill B1 Q8192 ctx32768", 1, 8192, 32768),
