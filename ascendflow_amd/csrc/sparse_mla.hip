@@ -130,25 +130,39 @@ __device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 15)
 // transposing LDS read are 4 apart and never share a 32-byte bank window.
 __device__ __forceinline__ int sigma(int m) { return ((m & 3) << 2) | (m >> 2); }
 
-template <int DT, int D, int NW>
-__global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
+// Lazy rescaling threshold (log2 units): the running max used for exp2 is only
+// raised, and O/l rescaled, once some head's max exceeds it by more than
+// TAU, so P stays <= 2^TAU; the final O/l is independent of the reference point.
+constexpr float TAU = 8.0f;
+
+// HG 16-head groups per workgroup (BM = 16*HG) and DS feature parts per head
+// group: wave w owns heads 16*(w % HG) and features [w / HG * D/DS, +D/DS).
+// With DS = 2 the two waves of a head group add their partial scores through
+// LDS, so each wave keeps only half of Q and half of O in registers.
+template <int DT, int D, int HG, int DS>
+__global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
   typedef typename B16<DT>::x4 x4;
+  constexpr int NW = HG * DS;
   constexpr int NT = NW * 64;
+  constexpr int DP = D / DS;                   // features per wave
   constexpr int UNITS = D / 8;                 // 16-byte units per row
   constexpr int PIECES = CHUNK * UNITS / NT;   // 16-byte loads per thread per chunk
   constexpr int ROW_BYTES = D * 2;
   static_assert(CHUNK * UNITS % NT == 0, "chunk must split evenly over the block");
   static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
+  static_assert(DP % 32 == 0, "feature part must hold whole k-steps");
 
   __shared__ __attribute__((aligned(16))) uint8_t kv_lds[2][CHUNK * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) f32x4 s_xchg[DS > 1 ? NW : 1][2][64];
   __shared__ int wave_count[NW];
-  extern __shared__ uint32_t row_list[];  // WINDOW + TOPK entries
+  extern __shared__ uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, i16 = lane & 15;
+  const int hg = wave % HG, part = wave / HG;
   const int head_tiles = a.H / a.BM;
   const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
   const int token = (int)(logical / head_tiles);
@@ -158,7 +172,6 @@ __global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
 
   // ---- 1. compact the selected rows into the LDS row list -------------------
   const int slots = a.WINDOW + geo.count_cmp;
-  const bool dump = a.debug_rows != nullptr && head0 == 0;
   int n_rows = 0;
   for (int s0 = 0; s0 < slots; s0 += NT) {
     const int s = s0 + tid;
@@ -181,7 +194,11 @@ __global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
     n_rows += total;
     __syncthreads();
   }
-  if (dump) {
+  // Pad the last chunk with a real row so every load is unconditional; the
+  // padded rows get -inf scores (P = 0) below.
+  const int chunks = (n_rows + CHUNK - 1) / CHUNK;
+  if (tid < chunks * CHUNK - n_rows) row_list[n_rows + tid] = row_list[0];
+  if (a.debug_rows != nullptr && head0 == 0) {
     for (int s = tid; s < a.S; s += NT) {
       uint32_t entry = 0;
       const bool valid = s < slots && resolve_slot(a, geo, token, s, entry);
@@ -190,37 +207,36 @@ __global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
       ((int2*)a.debug_rows)[(size_t)token * a.S + s] = v;
     }
   }
+  __syncthreads();
 
-  // ---- 2. Q fragments (B operand of S^T = KV * Q^T), resident all token ------
-  const int head = head0 + wave * 16 + i16;
-  const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + head) * D + 8 * g;
-  x8 qf[D / 32];
+  // ---- 2. Q fragments (B operand of S^T = KV * Q^T) for this wave's features
+  const int head = head0 + hg * 16 + i16;
+  const int dbase = part * DP;
+  const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + head) * D + dbase + 8 * g;
+  x8 qf[DP / 32];
 #pragma unroll
-  for (int j = 0; j < D / 32; ++j) qf[j] = *(const x8*)(q_row + 32 * j);
+  for (int j = 0; j < DP / 32; ++j) qf[j] = *(const x8*)(q_row + 32 * j);
 
-  f32x4 o[D / 16];
+  f32x4 o[DP / 16];
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < DP / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   float m_run = a.sinks[head] * LOG2E;  // sink seeds the running max
   float l_run = g == 0 ? 1.0f : 0.0f;   // e^(sink - m) counted once per head
   const float scale_log2 = a.scale * LOG2E;
 
   // ---- 3. chunk loop: global -> registers -> LDS, then QK, softmax, PV ------
-  const int chunks = (n_rows + CHUNK - 1) / CHUNK;
   u32x4 pf[PIECES];
+  const char* ori = (const char*)a.ori_kv;
+  const char* cmp = (const char*)a.cmp_kv;
   auto fetch = [&](int chunk) {
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) {
       const int flat = tid + p * NT;
       const int r = flat / UNITS, u = flat % UNITS;
-      const int row = chunk * CHUNK + r;
-      if (row < n_rows) {
-        const scalar* src = row_pointer<scalar>(a, row_list[row]);
-        pf[p] = *(const u32x4*)(src + u * 8);
-      } else {
-        pf[p] = u32x4{0u, 0u, 0u, 0u};
-      }
+      const uint32_t e = row_list[chunk * CHUNK + r];
+      const char* base = (e & CMP_BIT) ? cmp : ori;
+      pf[p] = *(const u32x4*)(base + (size_t)(e & ~CMP_BIT) * ROW_BYTES + u * 16);
     }
   };
   auto stash = [&](int buf) {
@@ -236,6 +252,7 @@ __global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
   const int rt = 4 * (i16 >> 2) + g;      // transposing-read row inside a tile
   const int tr_half = (i16 & 1) * 8;
   const int tr_unit = (i16 & 3) >> 1;
+  const int ubase = dbase / 8;            // first 16-byte unit of this wave's features
 
   if (chunks > 0) fetch(0);
   for (int c = 0; c < chunks; ++c) {
@@ -245,15 +262,31 @@ __global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
     if (c + 1 < chunks) fetch(c + 1);
     const uint8_t* tile = kv_lds[buf];
 
-    // S^T tiles: rows [0,16) and [16,32) of the chunk (permuted by sigma).
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    // Partial S^T tiles over this wave's features, two chains per row tile.
+    f32x4 s0a = {0.f, 0.f, 0.f, 0.f}, s0b = s0a, s1a = s0a, s1b = s0a;
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j) {
-      const int u = 4 * j + g;
-      const x8 a0 = *(const x8*)(tile + ra * ROW_BYTES + (swz(ra, u) << 4));
-      const x8 a1 = *(const x8*)(tile + (16 + ra) * ROW_BYTES + (swz(16 + ra, u) << 4));
-      s0 = B16<DT>::mfma(a0, qf[j], s0);
-      s1 = B16<DT>::mfma(a1, qf[j], s1);
+    for (int j = 0; j < DP / 32; j += 2) {
+      const int u0 = ubase + 4 * j + g, u1 = u0 + 4;
+      const x8 a00 = *(const x8*)(tile + ra * ROW_BYTES + (swz(ra, u0) << 4));
+      const x8 a10 = *(const x8*)(tile + (16 + ra) * ROW_BYTES + (swz(16 + ra, u0) << 4));
+      const x8 a01 = *(const x8*)(tile + ra * ROW_BYTES + (swz(ra, u1) << 4));
+      const x8 a11 = *(const x8*)(tile + (16 + ra) * ROW_BYTES + (swz(16 + ra, u1) << 4));
+      s0a = B16<DT>::mfma(a00, qf[j], s0a);
+      s1a = B16<DT>::mfma(a10, qf[j], s1a);
+      s0b = B16<DT>::mfma(a01, qf[j + 1], s0b);
+      s1b = B16<DT>::mfma(a11, qf[j + 1], s1b);
+    }
+    f32x4 s0 = s0a + s0b, s1 = s1a + s1b;
+    if constexpr (DS > 1) {
+      // Add the partner wave's partial scores (same heads, other features).
+      // Both waves form own + partner in the same commutative pair, so they
+      // hold bit-identical scores and take identical softmax decisions.
+      s_xchg[wave][0][lane] = s0;
+      s_xchg[wave][1][lane] = s1;
+      __syncthreads();
+      const int partner = (wave + HG) % NW;
+      s0 += s_xchg[partner][0][lane];
+      s1 += s_xchg[partner][1][lane];
     }
 
     // Online softmax for head `head`; this lane holds chunk rows 4i+g, 16+4i+g.
@@ -268,26 +301,32 @@ __global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
     }
     cmax = max_over_lane_groups(cmax);
     const float m_new = fmaxf(m_run, cmax);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
+    if (c == 0) {
+      l_run *= fast_exp2(m_run - m_new);  // O is still zero
+      m_run = m_new;
+    } else if (__ballot(m_new > m_run + TAU) != 0ull) {
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < DP / 16; ++t) o[t] *= alpha;
+      m_run = m_new;
+    }
     float psum = 0.f;
     x8 pf8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p0 = fast_exp2(x0[i] - m_new);
-      const float p1 = fast_exp2(x1[i] - m_new);
+      const float p0 = fast_exp2(x0[i] - m_run);
+      const float p1 = fast_exp2(x1[i] - m_run);
       psum += p0 + p1;
       pf8[i] = (scalar)p0;
       pf8[4 + i] = (scalar)p1;
     }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t) o[t] *= alpha;
+    l_run += psum;
 
-    // O^T[d, heads] += V^T[d, rows] * P^T[rows, heads].
+    // O^T[d, heads] += V^T[d, rows] * P^T[rows, heads] over this wave's features.
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t) {
-      const int u = 2 * t + tr_unit;
+    for (int t = 0; t < DP / 16; ++t) {
+      const int u = ubase + 2 * t + tr_unit;
       const x4 lo = B16<DT>::read_tr(
           (const AFA_LDS void*)(tile + rt * ROW_BYTES + (swz(rt, u) << 4) + tr_half));
       const x4 hi = B16<DT>::read_tr(
@@ -297,11 +336,11 @@ __global__ __launch_bounds__(NW * 64) void sparse_mla_kernel(SparseArgs a) {
     }
   }
 
-  // ---- 4. normalise and store: this lane holds d = 16t + 4g + i, head `head`.
+  // ---- 4. normalise and store: this lane holds d = dbase + 16t + 4g + i.
   const float inv = 1.0f / sum_over_lane_groups(l_run);
-  scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head) * D + 4 * g;
+  scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head) * D + dbase + 4 * g;
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t) {
+  for (int t = 0; t < DP / 16; ++t) {
     x4 v;
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = (scalar)(o[t][i] * inv);
@@ -390,21 +429,23 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   return a;
 }
 
-template <int DT, int D, int NW>
+template <int DT, int D, int HG, int DS>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
-  const size_t lds = (size_t)(a.WINDOW + a.TOPK) * sizeof(uint32_t);
+  const int list = (a.WINDOW + a.TOPK + CHUNK - 1) / CHUNK * CHUNK;
+  const size_t lds = (size_t)list * sizeof(uint32_t);
   const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
-  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NW>), dim3(blocks), dim3(NW * 64), lds, stream, a);
+  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, HG, DS>), dim3(blocks), dim3(HG * DS * 64), lds,
+                     stream, a);
   return (int)hipGetLastError();
 }
 
 template <int DT>
 static int dispatch_d(const SparseArgs& a, hipStream_t s) {
-  const int nw = a.BM / 16;
+  const bool four = a.BM == 64;
   switch (a.D) {
-    case 128: return nw == 4 ? launch_fused<DT, 128, 4>(a, s) : launch_fused<DT, 128, 2>(a, s);
-    case 256: return nw == 4 ? launch_fused<DT, 256, 4>(a, s) : launch_fused<DT, 256, 2>(a, s);
-    default: return nw == 4 ? launch_fused<DT, 512, 4>(a, s) : launch_fused<DT, 512, 2>(a, s);
+    case 128: return four ? launch_fused<DT, 128, 4, 1>(a, s) : launch_fused<DT, 128, 2, 1>(a, s);
+    case 256: return four ? launch_fused<DT, 256, 4, 2>(a, s) : launch_fused<DT, 256, 2, 2>(a, s);
+    default: return four ? launch_fused<DT, 512, 4, 2>(a, s) : launch_fused<DT, 512, 2, 2>(a, s);
   }
 }
 
