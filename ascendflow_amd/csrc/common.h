@@ -60,6 +60,21 @@ __device__ __forceinline__ float sum_over_lane_groups(float v) {
   return v;
 }
 
+// LDS has 32 four-byte banks (128 bytes per cycle). Unit u (16 bytes) of KV
+// row r lives at u ^ (r & 7): the eight 16-byte QK fragment reads served in
+// one cycle come from eight rows with distinct r & 7, and the four 32-byte
+// row pieces of one transposing read (16 lanes) come from rows whose
+// (r >> 1) & 3 differ, given the row permutation sigma below.
+__device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 7); }
+
+// Chunk row held at MFMA output row m = 4*g + q of a 16-row S^T tile:
+// sigma = 8*(g >> 1) + 2*q + (g & 1), i.e. lane groups 0..3 read the rows
+// {0,2,4,6}, {1,3,5,7}, {8,10,12,14}, {9,11,13,15} in their transposing reads.
+__device__ __forceinline__ int sigma(int m) {
+  const int g = m >> 2, q = m & 3;
+  return ((g >> 1) << 3) | (q << 1) | (g & 1);
+}
+
 // Blocks are dispatched round-robin over the 8 XCDs of an MI355X. Map the
 // hardware block id to a logical id so that each XCD receives a contiguous
 // range of logical ids (neighbouring work shares that XCD's L2).

@@ -33,8 +33,6 @@ struct FaArgs {
   float scale;
 };
 
-__device__ __forceinline__ int fa_swz(int row, int unit) { return unit ^ (row & 15); }
-__device__ __forceinline__ int fa_sigma(int m) { return ((m & 3) << 2) | (m >> 2); }
 
 // KC keys per LDS stage; NW waves; QT 16-row query tiles per wave; D = 128.
 template <int DT, int D, int NW, int QT, int KC>
@@ -119,14 +117,14 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) {
       const int flat = tid + p * NT, r = flat / UNITS, u = flat % UNITS;
-      const int off = r * ROW_BYTES + (fa_swz(r, u) << 4);
+      const int off = r * ROW_BYTES + (swz(r, u) << 4);
       *(u32x4*)(&k_lds[buf][off]) = pk[p];
       *(u32x4*)(&v_lds[buf][off]) = pv[p];
     }
   };
 
-  const int ra = fa_sigma(i16);
-  const int rt = 4 * (i16 >> 2) + g;
+  const int ra = sigma(i16);
+  const int rt = sigma(4 * g + (i16 >> 2));
   const int tr_half = (i16 & 1) * 8, tr_unit = (i16 & 3) >> 1;
 
   if (chunks > 0) fetch(0);
@@ -151,14 +149,14 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
 #pragma unroll
       for (int t = 0; t < KT; ++t) {
         const int row = 16 * t + ra;
-        const x8 kf = *(const x8*)(kt + row * ROW_BYTES + (fa_swz(row, u) << 4));
+        const x8 kf = *(const x8*)(kt + row * ROW_BYTES + (swz(row, u) << 4));
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) s[t][qt] = B16<DT>::mfma(kf, qf[qt][j], s[t][qt]);
       }
     }
 
     // Online softmax per query tile; this lane holds query q (column i16) and
-    // keys key0 + 16t + 4i + g.
+    // keys key0 + 16t + sigma(4g + i).
     x8 pf[QT][KC / 32];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -169,7 +167,7 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int64_t key = key0 + 16 * t + 4 * i + g;
+          const int64_t key = key0 + 16 * t + sigma(4 * g + i);
           const bool ok = key < a.Sk && (!a.causal || key <= query);
           x[t][i] = ok ? s[t][qt][i] * scale_log2 : -INFINITY;
           cmax = fmaxf(cmax, x[t][i]);
@@ -201,9 +199,9 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
         const int u = 2 * t + tr_unit;
         const int r0 = 32 * ks + rt, r1 = 32 * ks + 16 + rt;
         const x4 lo = B16<DT>::read_tr(
-            (const AFA_LDS void*)(vt + r0 * ROW_BYTES + (fa_swz(r0, u) << 4) + tr_half));
+            (const AFA_LDS void*)(vt + r0 * ROW_BYTES + (swz(r0, u) << 4) + tr_half));
         const x4 hi = B16<DT>::read_tr(
-            (const AFA_LDS void*)(vt + r1 * ROW_BYTES + (fa_swz(r1, u) << 4) + tr_half));
+            (const AFA_LDS void*)(vt + r1 * ROW_BYTES + (swz(r1, u) << 4) + tr_half));
         const x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) o[qt][t] = B16<DT>::mfma(vf, pf[qt][ks], o[qt][t]);
@@ -251,7 +249,7 @@ __global__ __launch_bounds__(256) void simple_attention_kernel(const _Float16* Q
 
   for (int flat = tid; flat < SK * (D / 8); flat += 256) {
     const int r = flat / (D / 8), u = flat % (D / 8);
-    const int off = r * ROW_BYTES + (fa_swz(r, u) << 4);
+    const int off = r * ROW_BYTES + (swz(r, u) << 4);
     *(u32x4*)(&k_lds[off]) = *(const u32x4*)(K + r * D + u * 8);
     *(u32x4*)(&v_lds[off]) = *(const u32x4*)(V + r * D + u * 8);
   }
@@ -261,7 +259,7 @@ __global__ __launch_bounds__(256) void simple_attention_kernel(const _Float16* Q
   for (int j = 0; j < D / 32; ++j) qf[j] = *(const f16x8*)(Q + query * D + 32 * j + 8 * g);
   __syncthreads();
 
-  const int ra = fa_sigma(i16);
+  const int ra = sigma(i16);
   f32x4 s[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -271,7 +269,7 @@ __global__ __launch_bounds__(256) void simple_attention_kernel(const _Float16* Q
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       const int row = 16 * t + ra;
-      const f16x8 kf = *(const f16x8*)(k_lds + row * ROW_BYTES + (fa_swz(row, u) << 4));
+      const f16x8 kf = *(const f16x8*)(k_lds + row * ROW_BYTES + (swz(row, u) << 4));
       s[t] = ops::mfma(kf, qf[j], s[t]);
     }
   }
@@ -300,7 +298,7 @@ __global__ __launch_bounds__(256) void simple_attention_kernel(const _Float16* Q
 #pragma unroll
     for (int i = 0; i < 4; ++i) pf[t >> 1][(t & 1) * 4 + i] = (_Float16)(s[t][i] * inv);
 
-  const int rt = 4 * (i16 >> 2) + g;
+  const int rt = sigma(4 * g + (i16 >> 2));
   const int tr_half = (i16 & 1) * 8, tr_unit = (i16 & 3) >> 1;
   _Float16* orow = O + query * D + 4 * g;
 #pragma unroll
@@ -311,9 +309,9 @@ __global__ __launch_bounds__(256) void simple_attention_kernel(const _Float16* Q
     for (int ks = 0; ks < SK / 32; ++ks) {
       const int r0 = 32 * ks + rt, r1 = 32 * ks + 16 + rt;
       const f16x4 lo = ops::read_tr(
-          (const AFA_LDS void*)(v_lds + r0 * ROW_BYTES + (fa_swz(r0, u) << 4) + tr_half));
+          (const AFA_LDS void*)(v_lds + r0 * ROW_BYTES + (swz(r0, u) << 4) + tr_half));
       const f16x4 hi = ops::read_tr(
-          (const AFA_LDS void*)(v_lds + r1 * ROW_BYTES + (fa_swz(r1, u) << 4) + tr_half));
+          (const AFA_LDS void*)(v_lds + r1 * ROW_BYTES + (swz(r1, u) << 4) + tr_half));
       const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       acc = ops::mfma(vf, pf[ks], acc);
     }

@@ -120,16 +120,6 @@ __device__ __forceinline__ const T* row_pointer(const SparseArgs& a, uint32_t en
   return base + (size_t)(entry & ~CMP_BIT) * a.D;
 }
 
-// XOR swizzle of 16-byte units inside an LDS row: unit u of row r lives at
-// u ^ (r & 15). Conflict-free for the QK fragment reads (16 distinct rows per
-// unit) and, with the row permutation sigma below, for the transposing PV reads.
-__device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 15); }
-
-// Row of a 16-row S^T tile held at MFMA output row m: the 4x4 transpose
-// sigma(m) = 4*(m % 4) + m / 4, so the four rows one lane group feeds into a
-// transposing LDS read are 4 apart and never share a 32-byte bank window.
-__device__ __forceinline__ int sigma(int m) { return ((m & 3) << 2) | (m >> 2); }
-
 // Lazy rescaling threshold (log2 units): the running max used for exp2 is only
 // raised, and O/l rescaled, once some head's max exceeds it by more than
 // TAU, so P stays <= 2^TAU; the final O/l is independent of the reference point.
@@ -249,7 +239,7 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   };
 
   const int ra = sigma(i16);              // QK fragment row inside a 16-row tile
-  const int rt = 4 * (i16 >> 2) + g;      // transposing-read row inside a tile
+  const int rt = sigma(4 * g + (i16 >> 2));  // transposing-read row inside a tile
   const int tr_half = (i16 & 1) * 8;
   const int tr_unit = (i16 & 3) >> 1;
   const int ubase = dbase / 8;            // first 16-byte unit of this wave's features
@@ -289,14 +279,16 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
       s1 += s_xchg[partner][1][lane];
     }
 
-    // Online softmax for head `head`; this lane holds chunk rows 4i+g, 16+4i+g.
+    // Online softmax for head `head`; this lane holds the chunk rows
+    // sigma(4g+i) and 16 + sigma(4g+i).
     const int live = n_rows - c * CHUNK;
     float x0[4], x1[4];
     float cmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x0[i] = (4 * i + g < live) ? s0[i] * scale_log2 : -INFINITY;
-      x1[i] = (16 + 4 * i + g < live) ? s1[i] * scale_log2 : -INFINITY;
+      const int row = sigma(4 * g + i);
+      x0[i] = (row < live) ? s0[i] * scale_log2 : -INFINITY;
+      x1[i] = (16 + row < live) ? s1[i] * scale_log2 : -INFINITY;
       cmax = fmaxf(cmax, fmaxf(x0[i], x1[i]));
     }
     cmax = max_over_lane_groups(cmax);
