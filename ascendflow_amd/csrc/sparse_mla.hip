@@ -25,6 +25,8 @@
 //
 // K and V are the same gathered rows; each row is read from global memory
 // once per workgroup and from LDS twice (once per contraction).
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/ascendflow_amd.h"
 
@@ -125,11 +127,36 @@ __device__ __forceinline__ const T* row_pointer(const SparseArgs& a, uint32_t en
 // TAU, so P stays <= 2^TAU; the final O/l is independent of the reference point.
 constexpr float TAU = 8.0f;
 
-// HG 16-head groups per workgroup (BM = 16*HG) and DS feature parts per head
-// group: wave w owns heads 16*(w % HG) and features [w / HG * D/DS, +D/DS).
-// With DS = 2 the two waves of a head group add their partial scores through
-// LDS, so each wave keeps only half of Q and half of O in registers.
-template <int DT, int D, int HG, int DS>
+// s_waitcnt immediate for lgkmcnt(0) alone (gfx9 encoding: vmcnt[3:0] |
+// expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14, all other fields at max).
+constexpr int WAIT_LGKM0 = 0xC07F;
+// Workgroup barrier without the memory fence of __syncthreads(): global loads
+// of later chunks stay in flight across it. The caller's own LDS stores are
+// complete (lgkmcnt(0)) before it signals; the empty asm statements keep the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+constexpr int NSTAGE = 3;  // KV chunk buffers in LDS
+constexpr int LOOK = 4;    // fragment-read lookahead (pipeline steps) in the PV/QK loop
+
+// Workgroup = one (token, BM-head tile). HG head groups of HT*16 heads and DS
+// feature parts: wave w owns heads [16*HT*(w % HG), +16*HT) and features
+// [(w / HG) * D/DS, +D/DS). Each KV fragment read from LDS feeds HT MFMAs (one
+// per 16-head tile). With DS > 1 the DS waves of a head group add their
+// partial scores through LDS, so each wave keeps only its share of Q and O.
+//
+// Software pipeline, one barrier per chunk c:
+//   stash KV(c+1) -> barrier -> fetch KV(c+2) -> exchange partial S(c) ->
+//   softmax(c) -> { QK(c+1) interleaved with PV(c) } -> publish partial S(c+1)
+// so the LDS reads and MFMAs of two chunks overlap. KV uses a ring of NSTAGE
+// buffers: when a wave stashes chunk c+1, the slowest wave is at worst still
+// reading chunks c-1 (PV) and c (QK), which live in the other two buffers.
+template <int DT, int D, int HG, int HT, int DS>
 __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
@@ -140,12 +167,13 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   constexpr int UNITS = D / 8;                 // 16-byte units per row
   constexpr int PIECES = CHUNK * UNITS / NT;   // 16-byte loads per thread per chunk
   constexpr int ROW_BYTES = D * 2;
+  constexpr int QK_STEPS = DP / 32, PV_STEPS = DP / 16;
   static_assert(CHUNK * UNITS % NT == 0, "chunk must split evenly over the block");
-  static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
-  static_assert(DP % 32 == 0, "feature part must hold whole k-steps");
+  static_assert(UNITS >= 8, "swizzle needs at least 8 units per row");
+  static_assert(DP % 32 == 0 && DP / 8 % 8 == 0, "feature part must hold whole k-steps");
 
-  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[2][CHUNK * ROW_BYTES];
-  __shared__ __attribute__((aligned(16))) f32x4 s_xchg[DS > 1 ? NW : 1][2][64];
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NSTAGE][CHUNK * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) f32x4 s_xchg[DS > 1 ? 2 : 1][DS > 1 ? NW : 1][DS > 1 ? 2 * HT : 1][64];
   __shared__ int wave_count[NW];
   extern __shared__ uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
@@ -200,22 +228,24 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   __syncthreads();
 
   // ---- 2. Q fragments (B operand of S^T = KV * Q^T) for this wave's features
-  const int head = head0 + hg * 16 + i16;
   const int dbase = part * DP;
-  const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + head) * D + dbase + 8 * g;
-  x8 qf[DP / 32];
+  const int hbase = head0 + hg * 16 * HT + i16;  // head of head tile ht: hbase + 16*ht
+  x8 qf[HT][QK_STEPS];
+  f32x4 o[HT][PV_STEPS];
+  float m_run[HT], l_run[HT];
 #pragma unroll
-  for (int j = 0; j < DP / 32; ++j) qf[j] = *(const x8*)(q_row + 32 * j);
-
-  f32x4 o[DP / 16];
+  for (int ht = 0; ht < HT; ++ht) {
+    const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + hbase + 16 * ht) * D + dbase + 8 * g;
 #pragma unroll
-  for (int t = 0; t < DP / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  float m_run = a.sinks[head] * LOG2E;  // sink seeds the running max
-  float l_run = g == 0 ? 1.0f : 0.0f;   // e^(sink - m) counted once per head
+    for (int j = 0; j < QK_STEPS; ++j) qf[ht][j] = *(const x8*)(q_row + 32 * j);
+#pragma unroll
+    for (int t = 0; t < PV_STEPS; ++t) o[ht][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[ht] = a.sinks[hbase + 16 * ht] * LOG2E;  // sink seeds the running max
+    l_run[ht] = g == 0 ? 1.0f : 0.0f;              // e^(sink - m) counted once per head
+  }
   const float scale_log2 = a.scale * LOG2E;
 
-  // ---- 3. chunk loop: global -> registers -> LDS, then QK, softmax, PV ------
+  // ---- 3. KV movement: global -> registers -> swizzled LDS rows --------------
   u32x4 pf[PIECES];
   const char* ori = (const char*)a.ori_kv;
   const char* cmp = (const char*)a.cmp_kv;
@@ -229,114 +259,188 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
       pf[p] = *(const u32x4*)(base + (size_t)(e & ~CMP_BIT) * ROW_BYTES + u * 16);
     }
   };
-  auto stash = [&](int buf) {
+  auto stash = [&](int chunk) {
+    uint8_t* tile = kv_lds[chunk % NSTAGE];
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) {
       const int flat = tid + p * NT;
       const int r = flat / UNITS, u = flat % UNITS;
-      *(u32x4*)(&kv_lds[buf][r * ROW_BYTES + (swz(r, u) << 4)]) = pf[p];
+      *(u32x4*)(&tile[r * ROW_BYTES + (swz(r, u) << 4)]) = pf[p];
     }
   };
 
-  const int ra = sigma(i16);              // QK fragment row inside a 16-row tile
-  const int rt = sigma(4 * g + (i16 >> 2));  // transposing-read row inside a tile
-  const int tr_half = (i16 & 1) * 8;
-  const int tr_unit = (i16 & 3) >> 1;
-  const int ubase = dbase / 8;            // first 16-byte unit of this wave's features
-
-  if (chunks > 0) fetch(0);
-  for (int c = 0; c < chunks; ++c) {
-    const int buf = c & 1;
-    stash(buf);
-    __syncthreads();
-    if (c + 1 < chunks) fetch(c + 1);
-    const uint8_t* tile = kv_lds[buf];
-
-    // Partial S^T tiles over this wave's features, two chains per row tile.
-    f32x4 s0a = {0.f, 0.f, 0.f, 0.f}, s0b = s0a, s1a = s0a, s1b = s0a;
+  // LDS byte offsets inside a chunk tile. The swizzle only permutes units
+  // within aligned groups of 8 (128 bytes), so every fragment address is a
+  // per-lane base (depending on j & 1 or t & 3) plus a compile-time offset.
+  const int ra = sigma(i16);                   // QK fragment row inside a 16-row tile
+  const int rt = sigma(4 * g + (i16 >> 2));    // transposing-read row inside a tile
+  const int ubase = dbase / 8;                 // first 16-byte unit of this wave's features
+  int qk_base[2], tr_base[4];
 #pragma unroll
-    for (int j = 0; j < DP / 32; j += 2) {
-      const int u0 = ubase + 4 * j + g, u1 = u0 + 4;
-      const x8 a00 = *(const x8*)(tile + ra * ROW_BYTES + (swz(ra, u0) << 4));
-      const x8 a10 = *(const x8*)(tile + (16 + ra) * ROW_BYTES + (swz(16 + ra, u0) << 4));
-      const x8 a01 = *(const x8*)(tile + ra * ROW_BYTES + (swz(ra, u1) << 4));
-      const x8 a11 = *(const x8*)(tile + (16 + ra) * ROW_BYTES + (swz(16 + ra, u1) << 4));
-      s0a = B16<DT>::mfma(a00, qf[j], s0a);
-      s1a = B16<DT>::mfma(a10, qf[j], s1a);
-      s0b = B16<DT>::mfma(a01, qf[j + 1], s0b);
-      s1b = B16<DT>::mfma(a11, qf[j + 1], s1b);
-    }
-    f32x4 s0 = s0a + s0b, s1 = s1a + s1b;
+  for (int b = 0; b < 2; ++b)
+    qk_base[b] = ra * ROW_BYTES + ubase * 16 + (((4 * b + g) ^ (ra & 7)) << 4);
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    tr_base[b] = rt * ROW_BYTES + ubase * 16 + (((2 * b + ((i16 & 3) >> 1)) ^ (rt & 7)) << 4) + (i16 & 1) * 8;
+
+  f32x4 s[2][HT];  // partial S^T [row tile][head tile] of the chunk QK last ran on
+  auto qk_zero = [&]() {
+#pragma unroll
+    for (int rtile = 0; rtile < 2; ++rtile)
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) s[rtile][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  // LDS-address-space view of a chunk tile: offsets fold into the DS
+  // instructions' immediate field.
+  auto lds_tile = [&](int chunk) { return (const AFA_LDS uint8_t*)kv_lds[chunk % NSTAGE]; };
+  auto publish = [&](int chunk) {
     if constexpr (DS > 1) {
-      // Add the partner wave's partial scores (same heads, other features).
-      // Both waves form own + partner in the same commutative pair, so they
-      // hold bit-identical scores and take identical softmax decisions.
-      s_xchg[wave][0][lane] = s0;
-      s_xchg[wave][1][lane] = s1;
-      __syncthreads();
-      const int partner = (wave + HG) % NW;
-      s0 += s_xchg[partner][0][lane];
-      s1 += s_xchg[partner][1][lane];
+#pragma unroll
+      for (int rtile = 0; rtile < 2; ++rtile)
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) s_xchg[chunk & 1][wave][rtile * HT + ht][lane] = s[rtile][ht];
     }
+  };
+  // Sum the DS partials in a fixed order: every wave of a head group then holds
+  // bit-identical scores and takes identical softmax decisions.
+  auto gather_scores = [&](int chunk) {
+    if constexpr (DS > 1) {
+#pragma unroll
+      for (int rtile = 0; rtile < 2; ++rtile)
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          f32x4 sum = s_xchg[chunk & 1][hg][rtile * HT + ht][lane];
+#pragma unroll
+          for (int p = 1; p < DS; ++p) sum += s_xchg[chunk & 1][hg + p * HG][rtile * HT + ht][lane];
+          s[rtile][ht] = sum;
+        }
+    }
+  };
 
-    // Online softmax for head `head`; this lane holds the chunk rows
-    // sigma(4g+i) and 16 + sigma(4g+i).
+  // One pipeline iteration for chunk c; MORE says whether chunk c + 1 exists.
+  auto iteration = [&](int c, auto more_tag) {
+    constexpr bool MORE = decltype(more_tag)::value;
+    if constexpr (MORE) stash(c + 1);
+    block_barrier();
+    if (c + 2 < chunks) fetch(c + 2);
+    gather_scores(c);
+
+    // Online softmax of chunk c per head tile; this lane holds the chunk rows
+    // sigma(4g+i) and 16 + sigma(4g+i) of head hbase + 16*ht. The running max
+    // starts at the sink and is raised (with O and l rescaled) only when a
+    // head's max exceeds it by more than TAU.
     const int live = n_rows - c * CHUNK;
-    float x0[4], x1[4];
-    float cmax = -INFINITY;
+    x8 pf8[HT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = sigma(4 * g + i);
-      x0[i] = (row < live) ? s0[i] * scale_log2 : -INFINITY;
-      x1[i] = (16 + row < live) ? s1[i] * scale_log2 : -INFINITY;
-      cmax = fmaxf(cmax, fmaxf(x0[i], x1[i]));
-    }
-    cmax = max_over_lane_groups(cmax);
-    const float m_new = fmaxf(m_run, cmax);
-    if (c == 0) {
-      l_run *= fast_exp2(m_run - m_new);  // O is still zero
-      m_run = m_new;
-    } else if (__ballot(m_new > m_run + TAU) != 0ull) {
-      const float alpha = fast_exp2(m_run - m_new);
-      l_run *= alpha;
+    for (int ht = 0; ht < HT; ++ht) {
+      float x0[4], x1[4];
+      float cmax = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < DP / 16; ++t) o[t] *= alpha;
-      m_run = m_new;
-    }
-    float psum = 0.f;
-    x8 pf8;
+      for (int i = 0; i < 4; ++i) {
+        const int row = sigma(4 * g + i);
+        x0[i] = (row < live) ? s[0][ht][i] * scale_log2 : -INFINITY;
+        x1[i] = (16 + row < live) ? s[1][ht][i] * scale_log2 : -INFINITY;
+        cmax = fmaxf(cmax, fmaxf(x0[i], x1[i]));
+      }
+      cmax = max_over_lane_groups(cmax);
+      const float m_new = fmaxf(m_run[ht], cmax);
+      if (__ballot(m_new > m_run[ht] + TAU) != 0ull) {
+        const float alpha = fast_exp2(m_run[ht] - m_new);
+        l_run[ht] *= alpha;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float p0 = fast_exp2(x0[i] - m_run);
-      const float p1 = fast_exp2(x1[i] - m_run);
-      psum += p0 + p1;
-      pf8[i] = (scalar)p0;
-      pf8[4 + i] = (scalar)p1;
+        for (int t = 0; t < PV_STEPS; ++t) o[ht][t] *= alpha;
+        m_run[ht] = m_new;
+      }
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p0 = fast_exp2(x0[i] - m_run[ht]);
+        const float p1 = fast_exp2(x1[i] - m_run[ht]);
+        psum += p0 + p1;
+        pf8[ht][i] = (scalar)p0;
+        pf8[ht][4 + i] = (scalar)p1;
+      }
+      l_run[ht] += psum;
     }
-    l_run += psum;
 
-    // O^T[d, heads] += V^T[d, rows] * P^T[rows, heads] over this wave's features.
+    // PV(c) interleaved with QK(c+1): step t runs PV d-tile t and, every
+    // RATIO_QK steps, one QK k-step. Fragment reads run LOOK steps ahead of
+    // their MFMAs; scheduling barriers pin that distance so the registers in
+    // flight stay bounded.
+    const AFA_LDS uint8_t* cur = lds_tile(c);
+    const AFA_LDS uint8_t* next = lds_tile(c + 1);
+    constexpr int RATIO_QK = PV_STEPS / QK_STEPS;
+    x4 vlo[PV_STEPS], vhi[PV_STEPS];
+    x8 ka0[QK_STEPS], ka1[QK_STEPS];
+    auto load_step = [&](int t) {
+      const AFA_LDS uint8_t* p = cur + tr_base[t & 3] + (t >> 2) * 128;
+      vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
+      vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
+      if (MORE && t % RATIO_QK == 0) {
+        const int j = t / RATIO_QK;
+        const AFA_LDS uint8_t* q = next + qk_base[j & 1] + (j >> 1) * 128;
+        ka0[j] = *(const AFA_LDS x8*)q;
+        ka1[j] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
+      }
+    };
+    if constexpr (MORE) qk_zero();
 #pragma unroll
-    for (int t = 0; t < DP / 16; ++t) {
-      const int u = ubase + 2 * t + tr_unit;
-      const x4 lo = B16<DT>::read_tr(
-          (const AFA_LDS void*)(tile + rt * ROW_BYTES + (swz(rt, u) << 4) + tr_half));
-      const x4 hi = B16<DT>::read_tr(
-          (const AFA_LDS void*)(tile + (16 + rt) * ROW_BYTES + (swz(16 + rt, u) << 4) + tr_half));
-      const x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      o[t] = B16<DT>::mfma(v, pf8, o[t]);
+    for (int t = 0; t < LOOK && t < PV_STEPS; ++t) load_step(t);
+#pragma unroll
+    for (int t = 0; t < PV_STEPS; ++t) {
+      if (t + LOOK < PV_STEPS) load_step(t + LOOK);
+      const x8 v = {vlo[t][0], vlo[t][1], vlo[t][2], vlo[t][3], vhi[t][0], vhi[t][1], vhi[t][2], vhi[t][3]};
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) o[ht][t] = B16<DT>::mfma(v, pf8[ht], o[ht][t]);
+      if (MORE && t % RATIO_QK == 0) {
+        const int j = t / RATIO_QK;
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          s[0][ht] = B16<DT>::mfma(ka0[j], qf[ht][j], s[0][ht]);
+          s[1][ht] = B16<DT>::mfma(ka1[j], qf[ht][j], s[1][ht]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (MORE) publish(c + 1);
+  };
+
+  // ---- 4. pipelined chunk loop ----------------------------------------------
+  if (chunks > 0) {
+    fetch(0);
+    stash(0);
+    if (chunks > 1) fetch(1);
+    block_barrier();
+    qk_zero();
+    const AFA_LDS uint8_t* first = lds_tile(0);
+#pragma unroll
+    for (int j = 0; j < QK_STEPS; ++j) {
+      const AFA_LDS uint8_t* q = first + qk_base[j & 1] + (j >> 1) * 128;
+      const x8 a0 = *(const AFA_LDS x8*)q;
+      const x8 a1 = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        s[0][ht] = B16<DT>::mfma(a0, qf[ht][j], s[0][ht]);
+        s[1][ht] = B16<DT>::mfma(a1, qf[ht][j], s[1][ht]);
+      }
+    }
+    publish(0);
+    for (int c = 0; c + 1 < chunks; ++c) iteration(c, std::true_type{});
+    iteration(chunks - 1, std::false_type{});
   }
 
-  // ---- 4. normalise and store: this lane holds d = dbase + 16t + 4g + i.
-  const float inv = 1.0f / sum_over_lane_groups(l_run);
-  scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head) * D + dbase + 4 * g;
+  // ---- 5. normalise and store: this lane holds d = dbase + 16t + 4g + i.
 #pragma unroll
-  for (int t = 0; t < DP / 16; ++t) {
-    x4 v;
+  for (int ht = 0; ht < HT; ++ht) {
+    const float inv = 1.0f / sum_over_lane_groups(l_run[ht]);
+    scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + hbase + 16 * ht) * D + dbase + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (scalar)(o[t][i] * inv);
-    *(x4*)(out_row + 16 * t) = v;
+    for (int t = 0; t < PV_STEPS; ++t) {
+      x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (scalar)(o[ht][t][i] * inv);
+      *(x4*)(out_row + 16 * t) = v;
+    }
   }
 }
 
@@ -421,23 +525,24 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   return a;
 }
 
-template <int DT, int D, int HG, int DS>
+template <int DT, int D, int HG, int HT, int DS>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   const int list = (a.WINDOW + a.TOPK + CHUNK - 1) / CHUNK * CHUNK;
   const size_t lds = (size_t)list * sizeof(uint32_t);
   const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
-  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, HG, DS>), dim3(blocks), dim3(HG * DS * 64), lds,
-                     stream, a);
+  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, HG, HT, DS>), dim3(blocks), dim3(HG * DS * 64),
+                     lds, stream, a);
   return (int)hipGetLastError();
 }
 
+// BM = 16 * HG * HT heads per workgroup.
 template <int DT>
 static int dispatch_d(const SparseArgs& a, hipStream_t s) {
   const bool four = a.BM == 64;
   switch (a.D) {
-    case 128: return four ? launch_fused<DT, 128, 4, 1>(a, s) : launch_fused<DT, 128, 2, 1>(a, s);
-    case 256: return four ? launch_fused<DT, 256, 4, 2>(a, s) : launch_fused<DT, 256, 2, 2>(a, s);
-    default: return four ? launch_fused<DT, 512, 4, 2>(a, s) : launch_fused<DT, 512, 2, 2>(a, s);
+    case 128: return four ? launch_fused<DT, 128, 2, 2, 1>(a, s) : launch_fused<DT, 128, 1, 2, 1>(a, s);
+    case 256: return four ? launch_fused<DT, 256, 2, 2, 2>(a, s) : launch_fused<DT, 256, 1, 2, 2>(a, s);
+    default: return four ? launch_fused<DT, 512, 4, 1, 2>(a, s) : launch_fused<DT, 512, 2, 1, 2>(a, s);
   }
 }
 
