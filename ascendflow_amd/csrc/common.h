@@ -47,17 +47,33 @@ template <> struct B16<DT_F16> {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Wave-wide reductions over the four lanes {l, l^16, l^32, l^48} that hold the
-// same MFMA output column.
+// Reductions over the four lanes {l, l^16, l^32, l^48} that hold the same
+// MFMA output column, with the gfx950 half-swaps v_permlane32_swap (lanes
+// 32..63 <-> 0..31) and v_permlane16_swap (16..31 <-> 0..15 in each half):
+// swapping a value with itself leaves each lane holding both partners.
+__device__ __forceinline__ void swap32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float max_over_lane_groups(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  float a, b;
+  swap16(v, a, b);
+  v = fmaxf(a, b);
+  swap32(v, a, b);
+  return fmaxf(a, b);
 }
 __device__ __forceinline__ float sum_over_lane_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  float a, b;
+  swap16(v, a, b);
+  v = a + b;
+  swap32(v, a, b);
+  return a + b;
 }
 
 // LDS has 32 four-byte banks (128 bytes per cycle). Unit u (16 bytes) of KV

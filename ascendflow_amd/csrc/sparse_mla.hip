@@ -142,7 +142,8 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 constexpr int NSTAGE = 3;  // KV chunk buffers in LDS
-constexpr int LOOK = 4;    // fragment-read lookahead (pipeline steps) in the PV/QK loop
+constexpr int LOOK = 4;     // V^T fragment-read lookahead (d-tiles) in the PV loop
+constexpr int LOOK_QK = 2;  // KV fragment-read lookahead (k-steps) in the QK loop
 
 // Workgroup = one (token, BM-head tile). HG head groups of HT*16 heads and DS
 // feature parts: wave w owns heads [16*HT*(w % HG), +16*HT) and features
@@ -188,7 +189,26 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
 
   const Geometry geo = token_geometry(a, token);
 
-  // ---- 1. compact the selected rows into the LDS row list -------------------
+  // ---- 1. Q fragments (B operand of S^T = KV * Q^T) for this wave's features,
+  // issued first so their latency overlaps the row-list construction
+  const int dbase = part * DP;
+  const int hbase = head0 + hg * 16 * HT + i16;  // head of head tile ht: hbase + 16*ht
+  x8 qf[HT][QK_STEPS];
+  f32x4 o[HT][PV_STEPS];
+  float m_run[HT], l_run[HT];
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+    const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + hbase + 16 * ht) * D + dbase + 8 * g;
+#pragma unroll
+    for (int j = 0; j < QK_STEPS; ++j) qf[ht][j] = *(const x8*)(q_row + 32 * j);
+#pragma unroll
+    for (int t = 0; t < PV_STEPS; ++t) o[ht][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[ht] = a.sinks[hbase + 16 * ht] * LOG2E;  // sink seeds the running max
+    l_run[ht] = g == 0 ? 1.0f : 0.0f;              // e^(sink - m) counted once per head
+  }
+  const float scale_log2 = a.scale * LOG2E;
+
+  // ---- 2. compact the selected rows into the LDS row list -------------------
   const int slots = a.WINDOW + geo.count_cmp;
   int n_rows = 0;
   for (int s0 = 0; s0 < slots; s0 += NT) {
@@ -226,24 +246,6 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     }
   }
   __syncthreads();
-
-  // ---- 2. Q fragments (B operand of S^T = KV * Q^T) for this wave's features
-  const int dbase = part * DP;
-  const int hbase = head0 + hg * 16 * HT + i16;  // head of head tile ht: hbase + 16*ht
-  x8 qf[HT][QK_STEPS];
-  f32x4 o[HT][PV_STEPS];
-  float m_run[HT], l_run[HT];
-#pragma unroll
-  for (int ht = 0; ht < HT; ++ht) {
-    const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + hbase + 16 * ht) * D + dbase + 8 * g;
-#pragma unroll
-    for (int j = 0; j < QK_STEPS; ++j) qf[ht][j] = *(const x8*)(q_row + 32 * j);
-#pragma unroll
-    for (int t = 0; t < PV_STEPS; ++t) o[ht][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_run[ht] = a.sinks[hbase + 16 * ht] * LOG2E;  // sink seeds the running max
-    l_run[ht] = g == 0 ? 1.0f : 0.0f;              // e^(sink - m) counted once per head
-  }
-  const float scale_log2 = a.scale * LOG2E;
 
   // ---- 3. KV movement: global -> registers -> swizzled LDS rows --------------
   u32x4 pf[PIECES];
@@ -317,6 +319,28 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     }
   };
 
+  // QK of one chunk into s, fragment reads LOOK_QK k-steps ahead of the MFMAs.
+  auto qk_chunk = [&](const AFA_LDS uint8_t* tile) {
+    x8 ka0[QK_STEPS], ka1[QK_STEPS];
+    auto load = [&](int j) {
+      const AFA_LDS uint8_t* q = tile + qk_base[j & 1] + (j >> 1) * 128;
+      ka0[j] = *(const AFA_LDS x8*)q;
+      ka1[j] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
+    };
+    qk_zero();
+#pragma unroll
+    for (int j = 0; j < LOOK_QK && j < QK_STEPS; ++j) load(j);
+#pragma unroll
+    for (int j = 0; j < QK_STEPS; ++j) {
+      if (j + LOOK_QK < QK_STEPS) load(j + LOOK_QK);
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        s[0][ht] = B16<DT>::mfma(ka0[j], qf[ht][j], s[0][ht]);
+        s[1][ht] = B16<DT>::mfma(ka1[j], qf[ht][j], s[1][ht]);
+      }
+    }
+  };
+
   // One pipeline iteration for chunk c; MORE says whether chunk c + 1 exists.
   auto iteration = [&](int c, auto more_tag) {
     constexpr bool MORE = decltype(more_tag)::value;
@@ -324,6 +348,14 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     block_barrier();
     if (c + 2 < chunks) fetch(c + 2);
     gather_scores(c);
+    f32x4 sc[2][HT];
+#pragma unroll
+    for (int rtile = 0; rtile < 2; ++rtile)
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) sc[rtile][ht] = s[rtile][ht];
+
+    // QK(c+1) is issued first so its MFMAs run under the softmax of chunk c.
+    if constexpr (MORE) qk_chunk(lds_tile(c + 1));
 
     // Online softmax of chunk c per head tile; this lane holds the chunk rows
     // sigma(4g+i) and 16 + sigma(4g+i) of head hbase + 16*ht. The running max
@@ -338,8 +370,8 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = sigma(4 * g + i);
-        x0[i] = (row < live) ? s[0][ht][i] * scale_log2 : -INFINITY;
-        x1[i] = (16 + row < live) ? s[1][ht][i] * scale_log2 : -INFINITY;
+        x0[i] = (row < live) ? sc[0][ht][i] * scale_log2 : -INFINITY;
+        x1[i] = (16 + row < live) ? sc[1][ht][i] * scale_log2 : -INFINITY;
         cmax = fmaxf(cmax, fmaxf(x0[i], x1[i]));
       }
       cmax = max_over_lane_groups(cmax);
@@ -362,28 +394,18 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
       }
       l_run[ht] += psum;
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MORE) publish(c + 1);
 
-    // PV(c) interleaved with QK(c+1): step t runs PV d-tile t and, every
-    // RATIO_QK steps, one QK k-step. Fragment reads run LOOK steps ahead of
-    // their MFMAs; scheduling barriers pin that distance so the registers in
-    // flight stay bounded.
+    // PV(c): V^T fragment reads LOOK steps ahead of their MFMAs; scheduling
+    // barriers pin that distance so the registers in flight stay bounded.
     const AFA_LDS uint8_t* cur = lds_tile(c);
-    const AFA_LDS uint8_t* next = lds_tile(c + 1);
-    constexpr int RATIO_QK = PV_STEPS / QK_STEPS;
     x4 vlo[PV_STEPS], vhi[PV_STEPS];
-    x8 ka0[QK_STEPS], ka1[QK_STEPS];
     auto load_step = [&](int t) {
       const AFA_LDS uint8_t* p = cur + tr_base[t & 3] + (t >> 2) * 128;
       vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
       vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
-      if (MORE && t % RATIO_QK == 0) {
-        const int j = t / RATIO_QK;
-        const AFA_LDS uint8_t* q = next + qk_base[j & 1] + (j >> 1) * 128;
-        ka0[j] = *(const AFA_LDS x8*)q;
-        ka1[j] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
-      }
     };
-    if constexpr (MORE) qk_zero();
 #pragma unroll
     for (int t = 0; t < LOOK && t < PV_STEPS; ++t) load_step(t);
 #pragma unroll
@@ -392,17 +414,8 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
       const x8 v = {vlo[t][0], vlo[t][1], vlo[t][2], vlo[t][3], vhi[t][0], vhi[t][1], vhi[t][2], vhi[t][3]};
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) o[ht][t] = B16<DT>::mfma(v, pf8[ht], o[ht][t]);
-      if (MORE && t % RATIO_QK == 0) {
-        const int j = t / RATIO_QK;
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht) {
-          s[0][ht] = B16<DT>::mfma(ka0[j], qf[ht][j], s[0][ht]);
-          s[1][ht] = B16<DT>::mfma(ka1[j], qf[ht][j], s[1][ht]);
-        }
-      }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (MORE) publish(c + 1);
   };
 
   // ---- 4. pipelined chunk loop ----------------------------------------------
@@ -411,19 +424,7 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     stash(0);
     if (chunks > 1) fetch(1);
     block_barrier();
-    qk_zero();
-    const AFA_LDS uint8_t* first = lds_tile(0);
-#pragma unroll
-    for (int j = 0; j < QK_STEPS; ++j) {
-      const AFA_LDS uint8_t* q = first + qk_base[j & 1] + (j >> 1) * 128;
-      const x8 a0 = *(const AFA_LDS x8*)q;
-      const x8 a1 = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        s[0][ht] = B16<DT>::mfma(a0, qf[ht][j], s[0][ht]);
-        s[1][ht] = B16<DT>::mfma(a1, qf[ht][j], s[1][ht]);
-      }
-    }
+    qk_chunk(lds_tile(0));
     publish(0);
     for (int c = 0; c + 1 < chunks; ++c) iteration(c, std::true_type{});
     iteration(chunks - 1, std::false_type{});
