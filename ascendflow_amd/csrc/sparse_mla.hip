@@ -305,18 +305,20 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   };
   // Sum the DS partials in a fixed order: every wave of a head group then holds
   // bit-identical scores and takes identical softmax decisions.
-  auto gather_scores = [&](int chunk) {
-    if constexpr (DS > 1) {
+  auto gather_scores = [&](int chunk, f32x4 (&out)[2][HT]) {
 #pragma unroll
-      for (int rtile = 0; rtile < 2; ++rtile)
+    for (int rtile = 0; rtile < 2; ++rtile)
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht) {
+      for (int ht = 0; ht < HT; ++ht) {
+        if constexpr (DS > 1) {
           f32x4 sum = s_xchg[chunk & 1][hg][rtile * HT + ht][lane];
 #pragma unroll
           for (int p = 1; p < DS; ++p) sum += s_xchg[chunk & 1][hg + p * HG][rtile * HT + ht][lane];
-          s[rtile][ht] = sum;
+          out[rtile][ht] = sum;
+        } else {
+          out[rtile][ht] = s[rtile][ht];
         }
-    }
+      }
   };
 
   // QK of one chunk into s, fragment reads LOOK_QK k-steps ahead of the MFMAs.
@@ -347,15 +349,23 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     if constexpr (MORE) stash(c + 1);
     block_barrier();
     if (c + 2 < chunks) fetch(c + 2);
-    gather_scores(c);
     f32x4 sc[2][HT];
-#pragma unroll
-    for (int rtile = 0; rtile < 2; ++rtile)
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) sc[rtile][ht] = s[rtile][ht];
+    gather_scores(c, sc);
 
     // QK(c+1) is issued first so its MFMAs run under the softmax of chunk c.
     if constexpr (MORE) qk_chunk(lds_tile(c + 1));
+
+    // First V^T fragments of PV(c) go out before the softmax, which they do
+    // not depend on.
+    const AFA_LDS uint8_t* cur = lds_tile(c);
+    x4 vlo[PV_STEPS], vhi[PV_STEPS];
+    auto load_step = [&](int t) {
+      const AFA_LDS uint8_t* p = cur + tr_base[t & 3] + (t >> 2) * 128;
+      vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
+      vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
+    };
+#pragma unroll
+    for (int t = 0; t < LOOK && t < PV_STEPS; ++t) load_step(t);
 
     // Online softmax of chunk c per head tile; this lane holds the chunk rows
     // sigma(4g+i) and 16 + sigma(4g+i) of head hbase + 16*ht. The running max
@@ -399,15 +409,6 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
 
     // PV(c): V^T fragment reads LOOK steps ahead of their MFMAs; scheduling
     // barriers pin that distance so the registers in flight stay bounded.
-    const AFA_LDS uint8_t* cur = lds_tile(c);
-    x4 vlo[PV_STEPS], vhi[PV_STEPS];
-    auto load_step = [&](int t) {
-      const AFA_LDS uint8_t* p = cur + tr_base[t & 3] + (t >> 2) * 128;
-      vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
-      vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
-    };
-#pragma unroll
-    for (int t = 0; t < LOOK && t < PV_STEPS; ++t) load_step(t);
 #pragma unroll
     for (int t = 0; t < PV_STEPS; ++t) {
       if (t + LOOK < PV_STEPS) load_step(t + LOOK);

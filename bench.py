@@ -96,6 +96,47 @@ def sparse_config(name, batch, queries, context, steps, warmup, flush, device):
     }
 
 
+def profiled_traffic(key):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary of this
+    workload (FETCH_SIZE + WRITE_SIZE, each scaled by a known-size copy)."""
+    import re
+
+    path = ROOT / "profiles" / f"sparse_mla_{key}.md"
+    if not path.exists():
+        return None
+    match = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", path.read_text(), re.M)
+    return int(match.group(1)) if match else None
+
+
+def attention_extras(steps, warmup, flush, device):
+    """Flash attention C2 (B1 H32 D128 S8192 f16) and teaching attention C1 timings."""
+    import torch
+
+    from ascendflow_amd.flash_attention import attention_target, simple_attention
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(9102201)
+    out = {}
+    q, k, v = (torch.randn((1, 32, 8192, 128), generator=gen, device=device).to(torch.float16) for _ in range(3))
+    o = torch.empty_like(q)
+    for causal in (False, True):
+        ms, _, _ = time_launches(lambda: attention_target(q, k, v, o, 8192, 8192, B=1, HQ=32, HKV=32, D=128, CAUSAL=causal),
+                                 steps, warmup, flush)
+        flops = 4 * 32 * 128 * (8192 * 8192 if not causal else 8192 * 8193 // 2)
+        tf = flops / (ms * 1e-3) / 1e12
+        out["fa_c2_causal" if causal else "fa_c2"] = {"ms": round(ms, 5), "tflops": round(tf, 2),
+                                                       "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
+        log(f"[bench] flash attention B1 H32 S8192 D128 f16 causal={causal}: {ms:.4f} ms, {tf:.1f} TFLOPS")
+    del q, k, v, o
+    qs = torch.randn((8, 1024, 128), generator=gen, device=device).to(torch.float16)
+    ks, vs = (torch.randn((8, 128, 128), generator=gen, device=device).to(torch.float16) for _ in range(2))
+    os_ = torch.empty_like(qs)
+    ms, _, _ = time_launches(lambda: simple_attention(qs, ks, vs, os_, S=1024, H=8), steps, warmup, flush)
+    out["simple_c1"] = {"ms": round(ms, 5), "tflops": round(4 * 8 * 1024 * 128 * 128 / (ms * 1e-3) / 1e12, 2)}
+    log(f"[bench] simple attention H8 S1024: {ms:.4f} ms")
+    return out
+
+
 def cpu_baseline(result, sample_tokens):
     """Time the oracle's vectorised FP32 PyTorch-CPU sparse MLA on a token sample."""
     import numpy as np
@@ -150,6 +191,7 @@ def main():
     parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k"], default=None,
                         help="time one configuration only (profiling runs)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-attention", action="store_true", help="skip the flash/teaching attention extras")
     parser.add_argument("--cpu-sample", type=int, default=1024, help="tokens in the CPU-baseline sample")
     parser.add_argument("--no-flush", action="store_true", help="keep caches warm between launches")
     parser.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -196,6 +238,10 @@ def main():
             results[key].pop("_inputs")  # free device memory of secondary configs
             torch.cuda.empty_cache()
 
+    extras = {}
+    if not args.only and not args.no_attention:
+        extras = attention_extras(args.steps, args.warmup, flush, device)
+
     head_key = order[0]
     head = results[head_key]
     baseline = None
@@ -232,12 +278,13 @@ def main():
             "peak": peak,
             "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(head_key),
         },
         "cpu_baseline": {k: v for k, v in baseline.items() if k != "ms_full_scaled"} if baseline else None,
         "extra": {k: {kk: vv for kk, vv in v.items() if kk != "_inputs"} for k, v in results.items()},
         "reference_ascend_910b3_ms": {"prefill8k": 6.847, "prefill32k": 27.225, "decode": 0.410},
     }
+    record["extra"].update(extras)
     if baseline:
         record["extra"]["cpu_ms_full_scaled"] = baseline["ms_full_scaled"]
     print(json.dumps(record), flush=True)
