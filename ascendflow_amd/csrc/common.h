@@ -76,20 +76,25 @@ __device__ __forceinline__ float sum_over_lane_groups(float v) {
   return a + b;
 }
 
-// LDS has 32 four-byte banks (128 bytes per cycle). Unit u (16 bytes) of KV
-// row r lives at u ^ (r & 7): the eight 16-byte QK fragment reads served in
-// one cycle come from eight rows with distinct r & 7, and the four 32-byte
-// row pieces of one transposing read (16 lanes) come from rows whose
-// (r >> 1) & 3 differ, given the row permutation sigma below.
-__device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 7); }
+// gfx950 LDS serves 64 four-byte banks (256 bytes) per cycle. Measured lane
+// grouping: a 16-byte read (ds_read_b128) serves, within each 32-lane half, the
+// 16 lanes whose quad index (lane >> 2) & 7 has even parity, then the odd ones;
+// an 8-byte transposing read (ds_read_b64_tr_b16) serves lanes 0..31, then
+// 32..63. Unit u (16 bytes) of KV row r lives at u ^ (r & 15). With the row
+// permutation sigma below:
+//  - QK fragment reads (lane (g, i) reads row sigma(i), unit 4j + g): each
+//    16-lane group touches 16 distinct 16-byte bank groups, because
+//    sigma({0..3} u {12..15}) and sigma({4..11}) are unions of row pairs
+//    {2k, 2k+1};
+//  - transposing reads (lane group g reads rows sigma(4g..4g+3), 32 bytes each):
+//    each 32-lane half touches 8 distinct 32-byte bank groups, because the
+//    rows of lane groups {0,1} and of {2,3} have distinct r >> 1.
+__device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 15); }
 
-// Chunk row held at MFMA output row m = 4*g + q of a 16-row S^T tile:
-// sigma = 8*(g >> 1) + 2*q + (g & 1), i.e. lane groups 0..3 read the rows
-// {0,2,4,6}, {1,3,5,7}, {8,10,12,14}, {9,11,13,15} in their transposing reads.
-__device__ __forceinline__ int sigma(int m) {
-  const int g = m >> 2, q = m & 3;
-  return ((g >> 1) << 3) | (q << 1) | (g & 1);
-}
+// Chunk row held at MFMA output row m of a 16-row S^T tile:
+// sigma(m) = 2*(m & 3) + {0, 8, 9, 1}[m >> 2], i.e. lane groups 0..3 of a
+// transposing read take the rows {0,2,4,6}, {8,10,12,14}, {9,11,13,15}, {1,3,5,7}.
+__device__ __forceinline__ int sigma(int m) { return ((m & 3) << 1) + ((0x1980 >> ((m >> 2) << 2)) & 15); }
 
 // Blocks are dispatched round-robin over the 8 XCDs of an MI355X. Map the
 // hardware block id to a logical id so that each XCD receives a contiguous

@@ -170,8 +170,8 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   constexpr int ROW_BYTES = D * 2;
   constexpr int QK_STEPS = DP / 32, PV_STEPS = DP / 16;
   static_assert(CHUNK * UNITS % NT == 0, "chunk must split evenly over the block");
-  static_assert(UNITS >= 8, "swizzle needs at least 8 units per row");
-  static_assert(DP % 32 == 0 && DP / 8 % 8 == 0, "feature part must hold whole k-steps");
+  static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
+  static_assert(DP % 32 == 0 && DP / 8 % 16 == 0, "feature part must hold whole swizzle groups");
 
   __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NSTAGE][CHUNK * ROW_BYTES];
   __shared__ __attribute__((aligned(16))) f32x4 s_xchg[DS > 1 ? 2 : 1][DS > 1 ? NW : 1][DS > 1 ? 2 * HT : 1][64];
@@ -272,18 +272,18 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   };
 
   // LDS byte offsets inside a chunk tile. The swizzle only permutes units
-  // within aligned groups of 8 (128 bytes), so every fragment address is a
-  // per-lane base (depending on j & 1 or t & 3) plus a compile-time offset.
+  // within aligned groups of 16 (256 bytes), so every fragment address is a
+  // per-lane base (depending on j & 3 or t & 7) plus a compile-time offset.
   const int ra = sigma(i16);                   // QK fragment row inside a 16-row tile
   const int rt = sigma(4 * g + (i16 >> 2));    // transposing-read row inside a tile
   const int ubase = dbase / 8;                 // first 16-byte unit of this wave's features
-  int qk_base[2], tr_base[4];
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-    qk_base[b] = ra * ROW_BYTES + ubase * 16 + (((4 * b + g) ^ (ra & 7)) << 4);
+  int qk_base[4], tr_base[8];
 #pragma unroll
   for (int b = 0; b < 4; ++b)
-    tr_base[b] = rt * ROW_BYTES + ubase * 16 + (((2 * b + ((i16 & 3) >> 1)) ^ (rt & 7)) << 4) + (i16 & 1) * 8;
+    qk_base[b] = ra * ROW_BYTES + ubase * 16 + (((4 * b + g) ^ (ra & 15)) << 4);
+#pragma unroll
+  for (int b = 0; b < 8; ++b)
+    tr_base[b] = rt * ROW_BYTES + ubase * 16 + (((2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8;
 
   f32x4 s[2][HT];  // partial S^T [row tile][head tile] of the chunk QK last ran on
   auto qk_zero = [&]() {
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   auto qk_chunk = [&](const AFA_LDS uint8_t* tile) {
     x8 ka0[QK_STEPS], ka1[QK_STEPS];
     auto load = [&](int j) {
-      const AFA_LDS uint8_t* q = tile + qk_base[j & 1] + (j >> 1) * 128;
+      const AFA_LDS uint8_t* q = tile + qk_base[j & 3] + (j >> 2) * 256;
       ka0[j] = *(const AFA_LDS x8*)q;
       ka1[j] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
     };
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     const AFA_LDS uint8_t* cur = lds_tile(c);
     x4 vlo[PV_STEPS], vhi[PV_STEPS];
     auto load_step = [&](int t) {
-      const AFA_LDS uint8_t* p = cur + tr_base[t & 3] + (t >> 2) * 128;
+      const AFA_LDS uint8_t* p = cur + tr_base[t & 7] + (t >> 3) * 256;
       vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
       vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
     };
