@@ -59,9 +59,11 @@ struct Geometry {
   int batch, right, visible, cutoff, count_cmp;
 };
 
-// query_metadata (gather.py:8-35) and the compressed bound (attention.py:339-341).
-__device__ __forceinline__ Geometry token_geometry(const SparseArgs& a, int token) {
-  int lo = 0, n = a.B;  // largest b in [0, B) with cu[b] <= token
+// Request of a token: upper_bound(cu_seqlens_q[0..B], token) - 1, i.e. the
+// last b in [0, B) with cu[b] <= token (gather.py:10-21; empty requests have
+// cu[b] == cu[b+1] and are skipped). Binary search, one thread.
+__device__ __forceinline__ int request_by_search(const SparseArgs& a, int token) {
+  int lo = 0, n = a.B;
   while (n > 1) {
     const int half = n >> 1;
     if (a.cu[lo + half] <= token) {
@@ -71,6 +73,31 @@ __device__ __forceinline__ Geometry token_geometry(const SparseArgs& a, int toke
       n = half;
     }
   }
+  return lo;
+}
+
+// The same request for a whole workgroup with one round of parallel loads:
+// since cu is non-decreasing and cu[0] = 0 <= token, the answer is
+// #{b in [0, B): cu[b] <= token} - 1.
+template <int NW>
+__device__ __forceinline__ int request_by_count(const SparseArgs& a, int token, int* scratch) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  int n = 0;
+  for (int b = tid; b < a.B; b += NW * 64) n += a.cu[b] <= token ? 1 : 0;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) n += __shfl_xor(n, d);
+  if (lane == 0) scratch[wave] = n;
+  __syncthreads();
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) total += scratch[w];
+  return total - 1;
+}
+
+// query_metadata (gather.py:8-35) and the compressed bound (attention.py:339-341)
+// of a token whose request is `batch`.
+__device__ __forceinline__ Geometry token_geometry(const SparseArgs& a, int token, int batch) {
+  const int lo = batch;
   Geometry g;
   g.batch = lo;
   const int begin = a.cu[lo], count = a.cu[lo + 1] - begin, offset = token - begin;
@@ -187,10 +214,8 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   const int token = (int)(logical / head_tiles);
   const int head0 = (int)(logical % head_tiles) * a.BM;
 
-  const Geometry geo = token_geometry(a, token);
-
   // ---- 1. Q fragments (B operand of S^T = KV * Q^T) for this wave's features,
-  // issued first so their latency overlaps the row-list construction
+  // issued first so their latency overlaps the request search and row list
   const int dbase = part * DP;
   const int hbase = head0 + hg * 16 * HT + i16;  // head of head tile ht: hbase + 16*ht
   x8 qf[HT][QK_STEPS];
@@ -207,6 +232,9 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     l_run[ht] = g == 0 ? 1.0f : 0.0f;              // e^(sink - m) counted once per head
   }
   const float scale_log2 = a.scale * LOG2E;
+
+  __shared__ int request_scratch[NW];
+  const Geometry geo = token_geometry(a, token, request_by_count<NW>(a, token, request_scratch));
 
   // ---- 2. compact the selected rows into the LDS row list -------------------
   const int slots = a.WINDOW + geo.count_cmp;
@@ -453,7 +481,7 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(SparseArgs a, void* 
                                                             float* bias_out) {
   typedef typename B16<DT>::scalar scalar;
   const int token = blockIdx.x;
-  const Geometry geo = token_geometry(a, token);
+  const Geometry geo = token_geometry(a, token, request_by_search(a, token));
   const int slots = a.WINDOW + geo.count_cmp;
   const int units = a.D / 8;
   for (int s = 0; s < a.S; ++s) {
