@@ -169,8 +169,8 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 constexpr int NSTAGE = 3;  // KV chunk buffers in LDS
-constexpr int LOOK = 4;     // V^T fragment-read lookahead (d-tiles) in the PV loop
-constexpr int LOOK_QK = 2;  // KV fragment-read lookahead (k-steps) in the QK loop
+constexpr int LOOK = 12;    // V^T fragment-read lookahead (d-tiles) in the PV loop
+constexpr int LOOK_QK = 4;  // KV fragment-read lookahead (k-steps) in the QK loop
 
 // Workgroup = one (token, BM-head tile). HG head groups of HT*16 heads and DS
 // feature parts: wave w owns heads [16*HT*(w % HG), +16*HT) and features
@@ -376,12 +376,13 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     constexpr bool MORE = decltype(more_tag)::value;
     if constexpr (MORE) stash(c + 1);
     block_barrier();
-    if (c + 2 < chunks) fetch(c + 2);
     f32x4 sc[2][HT];
     gather_scores(c, sc);
 
-    // QK(c+1) is issued first so its MFMAs run under the softmax of chunk c.
+    // QK(c+1) is issued first so its MFMAs run under the softmax of chunk c;
+    // the gather of chunk c+2 goes out behind it.
     if constexpr (MORE) qk_chunk(lds_tile(c + 1));
+    if (c + 2 < chunks) fetch(c + 2);
 
     // First V^T fragments of PV(c) go out before the softmax, which they do
     // not depend on.
