@@ -96,6 +96,30 @@ __device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 15)
 // transposing read take the rows {0,2,4,6}, {8,10,12,14}, {9,11,13,15}, {1,3,5,7}.
 __device__ __forceinline__ int sigma(int m) { return ((m & 3) << 1) + ((0x1980 >> ((m >> 2) << 2)) & 15); }
 
+// LDS byte address of a __shared__ object, and an LDS pointer from one.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const AFA_LDS void*)p;
+}
+template <typename T>
+__device__ __forceinline__ const AFA_LDS T* lds_at(uint32_t address) {
+  return (const AFA_LDS T*)(uintptr_t)address;
+}
+
+// Returns v unchanged but hides how it was formed. A per-iteration LDS base
+// laundered this way stays one register, and the constant parts of each
+// fragment address go into the DS instruction's offset field; without it the
+// compiler keeps one precomputed address per fragment and rebuilds each one
+// with two VALU operations every iteration.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  __asm__("" : "+v"(v));
+  return v;
+}
+// The same for a wave-uniform value, kept in a scalar register.
+__device__ __forceinline__ uint32_t opaque_uniform(uint32_t v) {
+  __asm__("" : "+s"(v));
+  return v;
+}
+
 // Blocks are dispatched round-robin over the 8 XCDs of an MI355X. Map the
 // hardware block id to a logical id so that each XCD receives a contiguous
 // range of logical ids (neighbouring work shares that XCD's L2).

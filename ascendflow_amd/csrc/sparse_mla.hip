@@ -206,7 +206,9 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   extern __shared__ uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // The wave index is uniform; readfirstlane lets the compiler see that, so
+  // branches on the wave's role are scalar branches.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int g = lane >> 4, i16 = lane & 15;
   const int hg = wave % HG, part = wave / HG;
   const int head_tiles = a.H / a.BM;
@@ -276,27 +278,50 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   __syncthreads();
 
   // ---- 3. KV movement: global -> registers -> swizzled LDS rows --------------
+  // Each wave moves PIECES rows of a chunk. With D = 512 one wave load covers
+  // exactly one 1 KiB row, so a wave takes PIECES consecutive rows whose list
+  // entries and addresses are wave-uniform (scalar registers); the lanes only
+  // add their 16-byte unit offset. Smaller D spreads one load over several rows.
+  constexpr bool ROW_LOADS = (UNITS == 64);
   u32x4 pf[PIECES];
   const char* ori = (const char*)a.ori_kv;
   const char* cmp = (const char*)a.cmp_kv;
-  auto fetch = [&](int chunk) {
+  const uint32_t kv_base = lds_address(kv_lds[0]);
+  auto tile_address = [&](int chunk) {
+    return opaque_uniform(kv_base + (uint32_t)(chunk % NSTAGE) * (CHUNK * ROW_BYTES));
+  };
+  // This lane's LDS offset inside a tile for piece p.
+  uint32_t stash_offset[PIECES];
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int flat = tid + p * NT;
-      const int r = flat / UNITS, u = flat % UNITS;
-      const uint32_t e = row_list[chunk * CHUNK + r];
-      const char* base = (e & CMP_BIT) ? cmp : ori;
-      pf[p] = *(const u32x4*)(base + (size_t)(e & ~CMP_BIT) * ROW_BYTES + u * 16);
+  for (int p = 0; p < PIECES; ++p) {
+    const int flat = ROW_LOADS ? (wave * PIECES + p) * UNITS + lane : tid + p * NT;
+    const int r = flat / UNITS, u = flat % UNITS;
+    stash_offset[p] = (uint32_t)(r * ROW_BYTES + (swz(r, u) << 4));
+  }
+  auto fetch = [&](int chunk) {
+    if constexpr (ROW_LOADS) {
+      const int first = chunk * CHUNK + wave * PIECES;
+#pragma unroll
+      for (int p = 0; p < PIECES; ++p) {
+        const uint32_t e = __builtin_amdgcn_readfirstlane(row_list[first + p]);
+        const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES;
+        pf[p] = *(const u32x4*)(row + lane * 16);
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < PIECES; ++p) {
+        const int flat = tid + p * NT;
+        const int r = flat / UNITS, u = flat % UNITS;
+        const uint32_t e = row_list[chunk * CHUNK + r];
+        const char* base = (e & CMP_BIT) ? cmp : ori;
+        pf[p] = *(const u32x4*)(base + (size_t)(e & ~CMP_BIT) * ROW_BYTES + u * 16);
+      }
     }
   };
   auto stash = [&](int chunk) {
-    uint8_t* tile = kv_lds[chunk % NSTAGE];
+    const uint32_t tile = tile_address(chunk);
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int flat = tid + p * NT;
-      const int r = flat / UNITS, u = flat % UNITS;
-      *(u32x4*)(&tile[r * ROW_BYTES + (swz(r, u) << 4)]) = pf[p];
-    }
+    for (int p = 0; p < PIECES; ++p) *(AFA_LDS u32x4*)lds_at<u32x4>(opaque(tile + stash_offset[p])) = pf[p];
   };
 
   // LDS byte offsets inside a chunk tile. The swizzle only permutes units
@@ -305,13 +330,13 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   const int ra = sigma(i16);                   // QK fragment row inside a 16-row tile
   const int rt = sigma(4 * g + (i16 >> 2));    // transposing-read row inside a tile
   const int ubase = dbase / 8;                 // first 16-byte unit of this wave's features
-  int qk_base[4], tr_base[8];
+  uint32_t qk_base[4], tr_base[8];
 #pragma unroll
   for (int b = 0; b < 4; ++b)
-    qk_base[b] = ra * ROW_BYTES + ubase * 16 + (((4 * b + g) ^ (ra & 15)) << 4);
+    qk_base[b] = (uint32_t)(ra * ROW_BYTES + ubase * 16 + (((4 * b + g) ^ (ra & 15)) << 4));
 #pragma unroll
   for (int b = 0; b < 8; ++b)
-    tr_base[b] = rt * ROW_BYTES + ubase * 16 + (((2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8;
+    tr_base[b] = (uint32_t)(rt * ROW_BYTES + ubase * 16 + (((2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
 
   f32x4 s[2][HT];  // partial S^T [row tile][head tile] of the chunk QK last ran on
   auto qk_zero = [&]() {
@@ -320,9 +345,6 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) s[rtile][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
-  // LDS-address-space view of a chunk tile: offsets fold into the DS
-  // instructions' immediate field.
-  auto lds_tile = [&](int chunk) { return (const AFA_LDS uint8_t*)kv_lds[chunk % NSTAGE]; };
   auto publish = [&](int chunk) {
     if constexpr (DS > 1) {
 #pragma unroll
@@ -331,29 +353,31 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
         for (int ht = 0; ht < HT; ++ht) s_xchg[chunk & 1][wave][rtile * HT + ht][lane] = s[rtile][ht];
     }
   };
-  // Sum the DS partials in a fixed order: every wave of a head group then holds
-  // bit-identical scores and takes identical softmax decisions.
+  // Full scores of the head group: the wave's own partial is still in s (QK of
+  // the next chunk has not run yet) and the other part's is read back. IEEE
+  // addition is commutative, so both waves of a head group hold bit-identical
+  // sums and take identical softmax decisions.
+  static_assert(DS <= 2, "score exchange assumes at most two feature parts");
   auto gather_scores = [&](int chunk, f32x4 (&out)[2][HT]) {
 #pragma unroll
     for (int rtile = 0; rtile < 2; ++rtile)
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) {
-        if constexpr (DS > 1) {
-          f32x4 sum = s_xchg[chunk & 1][hg][rtile * HT + ht][lane];
-#pragma unroll
-          for (int p = 1; p < DS; ++p) sum += s_xchg[chunk & 1][hg + p * HG][rtile * HT + ht][lane];
-          out[rtile][ht] = sum;
-        } else {
+        if constexpr (DS == 2)
+          out[rtile][ht] = s[rtile][ht] + s_xchg[chunk & 1][hg + (1 - part) * HG][rtile * HT + ht][lane];
+        else
           out[rtile][ht] = s[rtile][ht];
-        }
       }
   };
 
   // QK of one chunk into s, fragment reads LOOK_QK k-steps ahead of the MFMAs.
-  auto qk_chunk = [&](const AFA_LDS uint8_t* tile) {
+  auto qk_chunk = [&](uint32_t tile) {
     x8 ka0[QK_STEPS], ka1[QK_STEPS];
+    uint32_t base[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) base[b] = opaque(tile + qk_base[b]);
     auto load = [&](int j) {
-      const AFA_LDS uint8_t* q = tile + qk_base[j & 3] + (j >> 2) * 256;
+      const AFA_LDS uint8_t* q = lds_at<uint8_t>(base[j & 3]) + (j >> 2) * 256;
       ka0[j] = *(const AFA_LDS x8*)q;
       ka1[j] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
     };
@@ -379,60 +403,76 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     f32x4 sc[2][HT];
     gather_scores(c, sc);
 
-    // QK(c+1) is issued first so its MFMAs run under the softmax of chunk c;
-    // the gather of chunk c+2 goes out behind it.
-    if constexpr (MORE) qk_chunk(lds_tile(c + 1));
-    if (c + 2 < chunks) fetch(c + 2);
-
-    // First V^T fragments of PV(c) go out before the softmax, which they do
-    // not depend on.
-    const AFA_LDS uint8_t* cur = lds_tile(c);
+    // First V^T fragments of PV(c); they depend on neither QK(c+1) nor softmax(c).
+    uint32_t vbase[8];
     x4 vlo[PV_STEPS], vhi[PV_STEPS];
     auto load_step = [&](int t) {
-      const AFA_LDS uint8_t* p = cur + tr_base[t & 7] + (t >> 3) * 256;
+      const AFA_LDS uint8_t* p = lds_at<uint8_t>(vbase[t & 7]) + (t >> 3) * 256;
       vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
       vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
     };
+    auto v_first = [&]() {
+      const uint32_t tile = tile_address(c);
 #pragma unroll
-    for (int t = 0; t < LOOK && t < PV_STEPS; ++t) load_step(t);
+      for (int b = 0; b < 8; ++b) vbase[b] = opaque(tile + tr_base[b]);
+#pragma unroll
+      for (int t = 0; t < LOOK && t < PV_STEPS; ++t) load_step(t);
+    };
 
     // Online softmax of chunk c per head tile; this lane holds the chunk rows
     // sigma(4g+i) and 16 + sigma(4g+i) of head hbase + 16*ht. The running max
-    // starts at the sink and is raised (with O and l rescaled) only when a
-    // head's max exceeds it by more than TAU.
-    const int live = n_rows - c * CHUNK;
+    // (log2 units) starts at the sink and is raised (with O and l rescaled)
+    // only when a head's max exceeds it by more than TAU. Since the scale is
+    // positive, the chunk max is taken on the raw scores and the scale is
+    // applied inside the exponent's FMA. Only the last chunk holds padding.
     x8 pf8[HT];
+    auto softmax = [&]() {
+      const int live = n_rows - c * CHUNK;
 #pragma unroll
-    for (int ht = 0; ht < HT; ++ht) {
-      float x0[4], x1[4];
-      float cmax = -INFINITY;
+      for (int ht = 0; ht < HT; ++ht) {
+        float x0[4], x1[4];
+        float cmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = sigma(4 * g + i);
-        x0[i] = (row < live) ? sc[0][ht][i] * scale_log2 : -INFINITY;
-        x1[i] = (16 + row < live) ? sc[1][ht][i] * scale_log2 : -INFINITY;
-        cmax = fmaxf(cmax, fmaxf(x0[i], x1[i]));
+        for (int i = 0; i < 4; ++i) {
+          x0[i] = sc[0][ht][i];
+          x1[i] = sc[1][ht][i];
+          if constexpr (!MORE) {
+            const int row = sigma(4 * g + i);
+            x0[i] = (row < live) ? x0[i] : -INFINITY;
+            x1[i] = (16 + row < live) ? x1[i] : -INFINITY;
+          }
+          cmax = fmaxf(cmax, fmaxf(x0[i], x1[i]));
+        }
+        cmax = max_over_lane_groups(cmax);
+        const float m_new = fmaxf(m_run[ht], cmax * scale_log2);
+        if (__ballot(m_new > m_run[ht] + TAU) != 0ull) {
+          const float alpha = fast_exp2(m_run[ht] - m_new);
+          l_run[ht] *= alpha;
+#pragma unroll
+          for (int t = 0; t < PV_STEPS; ++t) o[ht][t] *= alpha;
+          m_run[ht] = m_new;
+        }
+        const float neg_m = -m_run[ht];
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p0 = fast_exp2(__builtin_fmaf(x0[i], scale_log2, neg_m));
+          const float p1 = fast_exp2(__builtin_fmaf(x1[i], scale_log2, neg_m));
+          psum += p0 + p1;
+          pf8[ht][i] = (scalar)p0;
+          pf8[ht][4 + i] = (scalar)p1;
+        }
+        l_run[ht] += psum;
       }
-      cmax = max_over_lane_groups(cmax);
-      const float m_new = fmaxf(m_run[ht], cmax);
-      if (__ballot(m_new > m_run[ht] + TAU) != 0ull) {
-        const float alpha = fast_exp2(m_run[ht] - m_new);
-        l_run[ht] *= alpha;
-#pragma unroll
-        for (int t = 0; t < PV_STEPS; ++t) o[ht][t] *= alpha;
-        m_run[ht] = m_new;
-      }
-      float psum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p0 = fast_exp2(x0[i] - m_run[ht]);
-        const float p1 = fast_exp2(x1[i] - m_run[ht]);
-        psum += p0 + p1;
-        pf8[ht][i] = (scalar)p0;
-        pf8[ht][4 + i] = (scalar)p1;
-      }
-      l_run[ht] += psum;
-    }
+    };
+
+    // QK(c+1) is issued first so its MFMAs run under the softmax of chunk c;
+    // the gather of chunk c+2 and the first V^T fragments of PV(c) go out
+    // before the softmax, which depends on neither.
+    if constexpr (MORE) qk_chunk(tile_address(c + 1));
+    if (c + 2 < chunks) fetch(c + 2);
+    v_first();
+    softmax();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (MORE) publish(c + 1);
 
@@ -454,7 +494,7 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
     stash(0);
     if (chunks > 1) fetch(1);
     block_barrier();
-    qk_chunk(lds_tile(0));
+    qk_chunk(tile_address(0));
     publish(0);
     for (int c = 0; c + 1 < chunks; ++c) iteration(c, std::true_type{});
     iteration(chunks - 1, std::false_type{});
