@@ -11,20 +11,21 @@
 //      (gather.py:8-35, attention.py:339-341) and compact every selected row
 //      (window positions, then compressed ranks, duplicates kept) into an LDS
 //      row list of physical row ids;
-//   2. stream the listed rows through a double-buffered, XOR-swizzled LDS
-//      tile of CHUNK rows with 16-byte coalesced loads (one wave reads whole
-//      1 KiB rows when D = 512);
-//   3. each wave owns 16 heads: S^T[rows, heads] = KV * Q^T on
-//      v_mfma_f32_16x16x32_{bf16,f16} with Q resident in registers;
-//   4. FP32 online softmax per head in registers (exp2 domain), the sink
-//      seeding the running max and contributing e^(sink-m) once;
-//   5. P (rounded to the storage dtype, round-to-nearest-even) feeds
-//      O^T[d, heads] += V^T * P^T directly from the S^T accumulators; V^T
-//      fragments come from the same LDS rows through ds_read_b64_tr_b16;
-//   6. O = O_acc * (1 / l), rounded to the storage dtype.
+//   2. stream the listed rows through a 3-stage ring of XOR-swizzled LDS
+//      tiles of CHUNK rows with the load-to-LDS path (global_load_lds_dwordx4,
+//      one wave load per 1 KiB row when D = 512);
+//   3. score waves (16 heads each, all D features of Q resident in registers):
+//      S^T[rows, heads] = KV * Q^T on v_mfma_f32_16x16x32_{bf16,f16}, FP32
+//      online softmax in the exp2 domain (the sink seeds the running max and
+//      contributes e^(sink-m) once), P rounded to the storage dtype
+//      (round-to-nearest-even) and handed over through LDS;
+//   4. output waves (all heads, D/NP features each): O^T[d, heads] +=
+//      V^T * P^T, V^T fragments from the same LDS rows through
+//      ds_read_b64_tr_b16;
+//   5. O = O_acc * (1 / l), rounded to the storage dtype.
 //
 // K and V are the same gathered rows; each row is read from global memory
-// once per workgroup and from LDS twice (once per contraction).
+// once per workgroup and from LDS once per score wave and once per output wave.
 #include <type_traits>
 
 #include "common.h"
@@ -169,71 +170,73 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 constexpr int NSTAGE = 3;  // KV chunk buffers in LDS
-constexpr int LOOK = 12;    // V^T fragment-read lookahead (d-tiles) in the PV loop
-constexpr int LOOK_QK = 4;  // KV fragment-read lookahead (k-steps) in the QK loop
+constexpr int LOOK = 4;     // V^T fragment lookahead (16-feature tiles) of an output wave
+constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
 
-// Workgroup = one (token, BM-head tile). HG head groups of HT*16 heads and DS
-// feature parts: wave w owns heads [16*HT*(w % HG), +16*HT) and features
-// [(w / HG) * D/DS, +D/DS). Each KV fragment read from LDS feeds HT MFMAs (one
-// per 16-head tile). With DS > 1 the DS waves of a head group add their
-// partial scores through LDS, so each wave keeps only its share of Q and O.
+// Workgroup = one (token, BM-head tile), BM = 16 * NQ, split by role:
+//  - score wave q < NQ owns heads [16q, 16q + 16) with all D features of Q
+//    resident: S^T = KV * Q^T for the chunk, FP32 online softmax, and the
+//    rounded P written to LDS in the MFMA B-operand layout;
+//  - output wave p owns features [p * D/NP, +D/NP) of all BM heads:
+//    O^T += V^T * P^T, so every V^T fragment read from LDS feeds NQ MFMAs.
+// No partial scores are exchanged, each KV row is read from LDS once per score
+// wave and once per output wave, and the softmax VALU work sits on score waves
+// only. Waves w and w + 4 of a 512-thread workgroup share a SIMD (measured
+// dispatch order), so with NQ = NP = 4 every SIMD runs one wave of each role
+// and their LDS, VALU and MFMA phases interleave.
 //
-// Software pipeline, one barrier per chunk c:
-//   stash KV(c+1) -> barrier -> fetch KV(c+2) -> exchange partial S(c) ->
-//   softmax(c) -> { QK(c+1) interleaved with PV(c) } -> publish partial S(c+1)
-// so the LDS reads and MFMAs of two chunks overlap. KV uses a ring of NSTAGE
-// buffers: when a wave stashes chunk c+1, the slowest wave is at worst still
-// reading chunks c-1 (PV) and c (QK), which live in the other two buffers.
-template <int DT, int D, int HG, int HT, int DS>
-__global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) {
+// Software pipeline, one barrier per step i = 0..chunks:
+//   stash KV(i) -> barrier -> fetch KV(i+1) -> score waves: QK(i), softmax(i),
+//   P(i) -> LDS slot i&1; output waves: PV(i-1) from slot (i-1)&1.
+// KV uses a ring of NSTAGE buffers: during step i the score waves read tile i
+// and the output waves tile i-1, so the stash of tile i+1 at the top of step
+// i+1 never overwrites a tile still in use.
+template <int DT, int D, int NQ, int NP>
+__global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
   typedef typename B16<DT>::x4 x4;
-  constexpr int NW = HG * DS;
+  constexpr int NW = NQ + NP;
   constexpr int NT = NW * 64;
-  constexpr int DP = D / DS;                   // features per wave
+  constexpr int BMH = 16 * NQ;                 // heads per workgroup
   constexpr int UNITS = D / 8;                 // 16-byte units per row
   constexpr int PIECES = CHUNK * UNITS / NT;   // 16-byte loads per thread per chunk
   constexpr int ROW_BYTES = D * 2;
-  constexpr int QK_STEPS = DP / 32, PV_STEPS = DP / 16;
+  constexpr int QK_STEPS = D / 32;             // k-steps of a score wave
+  constexpr int DPV = D / NP;                  // features per output wave
+  constexpr int PVT = DPV / 16;                // 16-feature tiles per output wave
   static_assert(CHUNK * UNITS % NT == 0, "chunk must split evenly over the block");
   static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
-  static_assert(DP % 32 == 0 && DP / 8 % 16 == 0, "feature part must hold whole swizzle groups");
+  static_assert(DPV % 16 == 0 && (PVT <= 8 || (DPV / 8) % 16 == 0), "output feature range");
 
   __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NSTAGE][CHUNK * ROW_BYTES];
-  __shared__ __attribute__((aligned(16))) f32x4 s_xchg[DS > 1 ? 2 : 1][DS > 1 ? NW : 1][DS > 1 ? 2 * HT : 1][64];
+  __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][NQ][64];  // P in B-operand layout
+  __shared__ float alpha_lds[2][BMH];   // O rescale factor per head, valid when flagged
+  __shared__ __attribute__((aligned(16))) int flag_lds[2][4];  // score wave q raised its running max
+  __shared__ float linv_lds[BMH];       // 1 / softmax denominator per head
   __shared__ int wave_count[NW];
-  extern __shared__ uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
+  extern __shared__ __attribute__((aligned(16))) uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
   const int tid = threadIdx.x;
   // The wave index is uniform; readfirstlane lets the compiler see that, so
   // branches on the wave's role are scalar branches.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int g = lane >> 4, i16 = lane & 15;
-  const int hg = wave % HG, part = wave / HG;
+  const bool scorer = wave < NQ;
   const int head_tiles = a.H / a.BM;
   const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
   const int token = (int)(logical / head_tiles);
   const int head0 = (int)(logical % head_tiles) * a.BM;
 
-  // ---- 1. Q fragments (B operand of S^T = KV * Q^T) for this wave's features,
-  // issued first so their latency overlaps the request search and row list
-  const int dbase = part * DP;
-  const int hbase = head0 + hg * 16 * HT + i16;  // head of head tile ht: hbase + 16*ht
-  x8 qf[HT][QK_STEPS];
-  f32x4 o[HT][PV_STEPS];
-  float m_run[HT], l_run[HT];
+  // ---- 1. Q fragments of a score wave (B operand of S^T = KV * Q^T), issued
+  // first so their latency overlaps the request search and the row list.
+  const int qhead = head0 + 16 * wave + i16;   // score wave: this lane's head
+  x8 qf[QK_STEPS];
+  if (scorer) {
+    const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + qhead) * D + 8 * g;
 #pragma unroll
-  for (int ht = 0; ht < HT; ++ht) {
-    const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + hbase + 16 * ht) * D + dbase + 8 * g;
-#pragma unroll
-    for (int j = 0; j < QK_STEPS; ++j) qf[ht][j] = *(const x8*)(q_row + 32 * j);
-#pragma unroll
-    for (int t = 0; t < PV_STEPS; ++t) o[ht][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_run[ht] = a.sinks[hbase + 16 * ht] * LOG2E;  // sink seeds the running max
-    l_run[ht] = g == 0 ? 1.0f : 0.0f;              // e^(sink - m) counted once per head
+    for (int j = 0; j < QK_STEPS; ++j) qf[j] = *(const x8*)(q_row + 32 * j);
   }
-  const float scale_log2 = a.scale * LOG2E;
 
   __shared__ int request_scratch[NW];
   const Geometry geo = token_geometry(a, token, request_by_count<NW>(a, token, request_scratch));
@@ -277,240 +280,229 @@ __global__ __launch_bounds__(HG * DS * 64) void sparse_mla_kernel(SparseArgs a) 
   }
   __syncthreads();
 
-  // ---- 3. KV movement: global -> registers -> swizzled LDS rows --------------
-  // Each wave moves PIECES rows of a chunk. With D = 512 one wave load covers
-  // exactly one 1 KiB row, so a wave takes PIECES consecutive rows whose list
-  // entries and addresses are wave-uniform (scalar registers); the lanes only
-  // add their 16-byte unit offset. Smaller D spreads one load over several rows.
+  // ---- 3. KV movement: global -> LDS through the load-to-LDS path ------------
+  // global_load_lds_dwordx4 writes one wave's 64 x 16 bytes contiguously at the
+  // LDS address in M0. The XOR swizzle is applied on the global side (the lane
+  // that lands on unit position u of row r loads unit u ^ (r & 15)), so LDS
+  // holds the swizzled rows without VGPR staging or ds_write traffic. M0 is
+  // set inside the same asm statement; nothing else in this kernel uses M0.
+  // Completion is tracked with vmcnt: when a step waits, the only vector
+  // memory loads in flight are the previous fetch's.
+  // With D = 512 one wave load covers exactly one 1 KiB row, so a wave takes
+  // PIECES consecutive rows whose list entries and addresses are wave-uniform
+  // (scalar registers), and the entries are read one step ahead.
   constexpr bool ROW_LOADS = (UNITS == 64);
-  u32x4 pf[PIECES];
   const char* ori = (const char*)a.ori_kv;
   const char* cmp = (const char*)a.cmp_kv;
   const uint32_t kv_base = lds_address(kv_lds[0]);
   auto tile_address = [&](int chunk) {
     return opaque_uniform(kv_base + (uint32_t)(chunk % NSTAGE) * (CHUNK * ROW_BYTES));
   };
-  // This lane's LDS offset inside a tile for piece p.
-  uint32_t stash_offset[PIECES];
+  uint32_t unit_offset[PIECES];  // ROW_LOADS: byte offset of the unit this lane loads
 #pragma unroll
-  for (int p = 0; p < PIECES; ++p) {
-    const int flat = ROW_LOADS ? (wave * PIECES + p) * UNITS + lane : tid + p * NT;
-    const int r = flat / UNITS, u = flat % UNITS;
-    stash_offset[p] = (uint32_t)(r * ROW_BYTES + (swz(r, u) << 4));
-  }
+  for (int p = 0; p < PIECES; ++p) unit_offset[p] = (uint32_t)((lane ^ ((wave * PIECES + p) & 15)) << 4);
+  uint32_t entry_next[PIECES];
+  auto read_entries = [&](int chunk) {
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) entry_next[p] = row_list[chunk * CHUNK + wave * PIECES + p];
+  };
   auto fetch = [&](int chunk) {
+    const uint32_t tile = tile_address(chunk);
     if constexpr (ROW_LOADS) {
-      const int first = chunk * CHUNK + wave * PIECES;
 #pragma unroll
       for (int p = 0; p < PIECES; ++p) {
-        const uint32_t e = __builtin_amdgcn_readfirstlane(row_list[first + p]);
+        const int r = wave * PIECES + p;
+        const uint32_t e = __builtin_amdgcn_readfirstlane(entry_next[p]);
         const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES;
-        pf[p] = *(const u32x4*)(row + lane * 16);
+        const uint32_t dst = tile + (uint32_t)(r * ROW_BYTES);
+        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                         :: "s"(dst), "v"(unit_offset[p]), "s"(row) : "memory");
       }
+      if (chunk + 1 < chunks) read_entries(chunk + 1);
     } else {
 #pragma unroll
       for (int p = 0; p < PIECES; ++p) {
         const int flat = tid + p * NT;
-        const int r = flat / UNITS, u = flat % UNITS;
+        const int r = flat / UNITS, upos = flat % UNITS;
         const uint32_t e = row_list[chunk * CHUNK + r];
-        const char* base = (e & CMP_BIT) ? cmp : ori;
-        pf[p] = *(const u32x4*)(base + (size_t)(e & ~CMP_BIT) * ROW_BYTES + u * 16);
+        const char* src = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES + ((upos ^ (r & 15)) << 4);
+        const uint32_t dst = tile + (uint32_t)((wave * 64 + p * NT) * 16);
+        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                         :: "s"(dst), "v"(src) : "memory");
       }
     }
   };
-  auto stash = [&](int chunk) {
-    const uint32_t tile = tile_address(chunk);
-#pragma unroll
-    for (int p = 0; p < PIECES; ++p) *(AFA_LDS u32x4*)lds_at<u32x4>(opaque(tile + stash_offset[p])) = pf[p];
-  };
-
-  // LDS byte offsets inside a chunk tile. The swizzle only permutes units
-  // within aligned groups of 16 (256 bytes), so every fragment address is a
-  // per-lane base (depending on j & 3 or t & 7) plus a compile-time offset.
-  const int ra = sigma(i16);                   // QK fragment row inside a 16-row tile
-  const int rt = sigma(4 * g + (i16 >> 2));    // transposing-read row inside a tile
-  const int ubase = dbase / 8;                 // first 16-byte unit of this wave's features
-  uint32_t qk_base[4], tr_base[8];
-#pragma unroll
-  for (int b = 0; b < 4; ++b)
-    qk_base[b] = (uint32_t)(ra * ROW_BYTES + ubase * 16 + (((4 * b + g) ^ (ra & 15)) << 4));
-#pragma unroll
-  for (int b = 0; b < 8; ++b)
-    tr_base[b] = (uint32_t)(rt * ROW_BYTES + ubase * 16 + (((2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
-
-  f32x4 s[2][HT];  // partial S^T [row tile][head tile] of the chunk QK last ran on
-  auto qk_zero = [&]() {
-#pragma unroll
-    for (int rtile = 0; rtile < 2; ++rtile)
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) s[rtile][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
-  };
-  auto publish = [&](int chunk) {
-    if constexpr (DS > 1) {
-#pragma unroll
-      for (int rtile = 0; rtile < 2; ++rtile)
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht) s_xchg[chunk & 1][wave][rtile * HT + ht][lane] = s[rtile][ht];
-    }
-  };
-  // Full scores of the head group: the wave's own partial is still in s (QK of
-  // the next chunk has not run yet) and the other part's is read back. IEEE
-  // addition is commutative, so both waves of a head group hold bit-identical
-  // sums and take identical softmax decisions.
-  static_assert(DS <= 2, "score exchange assumes at most two feature parts");
-  auto gather_scores = [&](int chunk, f32x4 (&out)[2][HT]) {
-#pragma unroll
-    for (int rtile = 0; rtile < 2; ++rtile)
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        if constexpr (DS == 2)
-          out[rtile][ht] = s[rtile][ht] + s_xchg[chunk & 1][hg + (1 - part) * HG][rtile * HT + ht][lane];
-        else
-          out[rtile][ht] = s[rtile][ht];
-      }
-  };
-
-  // QK of one chunk into s, fragment reads LOOK_QK k-steps ahead of the MFMAs.
-  auto qk_chunk = [&](uint32_t tile) {
-    x8 ka0[QK_STEPS], ka1[QK_STEPS];
-    uint32_t base[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) base[b] = opaque(tile + qk_base[b]);
-    auto load = [&](int j) {
-      const AFA_LDS uint8_t* q = lds_at<uint8_t>(base[j & 3]) + (j >> 2) * 256;
-      ka0[j] = *(const AFA_LDS x8*)q;
-      ka1[j] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
-    };
-    qk_zero();
-#pragma unroll
-    for (int j = 0; j < LOOK_QK && j < QK_STEPS; ++j) load(j);
-#pragma unroll
-    for (int j = 0; j < QK_STEPS; ++j) {
-      if (j + LOOK_QK < QK_STEPS) load(j + LOOK_QK);
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        s[0][ht] = B16<DT>::mfma(ka0[j], qf[ht][j], s[0][ht]);
-        s[1][ht] = B16<DT>::mfma(ka1[j], qf[ht][j], s[1][ht]);
-      }
-    }
-  };
-
-  // One pipeline iteration for chunk c; MORE says whether chunk c + 1 exists.
-  auto iteration = [&](int c, auto more_tag) {
-    constexpr bool MORE = decltype(more_tag)::value;
-    if constexpr (MORE) stash(c + 1);
-    block_barrier();
-    f32x4 sc[2][HT];
-    gather_scores(c, sc);
-
-    // First V^T fragments of PV(c); they depend on neither QK(c+1) nor softmax(c).
-    uint32_t vbase[8];
-    x4 vlo[PV_STEPS], vhi[PV_STEPS];
-    auto load_step = [&](int t) {
-      const AFA_LDS uint8_t* p = lds_at<uint8_t>(vbase[t & 7]) + (t >> 3) * 256;
-      vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
-      vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
-    };
-    auto v_first = [&]() {
-      const uint32_t tile = tile_address(c);
-#pragma unroll
-      for (int b = 0; b < 8; ++b) vbase[b] = opaque(tile + tr_base[b]);
-#pragma unroll
-      for (int t = 0; t < LOOK && t < PV_STEPS; ++t) load_step(t);
-    };
-
-    // Online softmax of chunk c per head tile; this lane holds the chunk rows
-    // sigma(4g+i) and 16 + sigma(4g+i) of head hbase + 16*ht. The running max
-    // (log2 units) starts at the sink and is raised (with O and l rescaled)
-    // only when a head's max exceeds it by more than TAU. Since the scale is
-    // positive, the chunk max is taken on the raw scores and the scale is
-    // applied inside the exponent's FMA. Only the last chunk holds padding.
-    x8 pf8[HT];
-    auto softmax = [&]() {
-      const int live = n_rows - c * CHUNK;
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        float x0[4], x1[4];
-        float cmax = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x0[i] = sc[0][ht][i];
-          x1[i] = sc[1][ht][i];
-          if constexpr (!MORE) {
-            const int row = sigma(4 * g + i);
-            x0[i] = (row < live) ? x0[i] : -INFINITY;
-            x1[i] = (16 + row < live) ? x1[i] : -INFINITY;
-          }
-          cmax = fmaxf(cmax, fmaxf(x0[i], x1[i]));
-        }
-        cmax = max_over_lane_groups(cmax);
-        const float m_new = fmaxf(m_run[ht], cmax * scale_log2);
-        if (__ballot(m_new > m_run[ht] + TAU) != 0ull) {
-          const float alpha = fast_exp2(m_run[ht] - m_new);
-          l_run[ht] *= alpha;
-#pragma unroll
-          for (int t = 0; t < PV_STEPS; ++t) o[ht][t] *= alpha;
-          m_run[ht] = m_new;
-        }
-        const float neg_m = -m_run[ht];
-        float psum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p0 = fast_exp2(__builtin_fmaf(x0[i], scale_log2, neg_m));
-          const float p1 = fast_exp2(__builtin_fmaf(x1[i], scale_log2, neg_m));
-          psum += p0 + p1;
-          pf8[ht][i] = (scalar)p0;
-          pf8[ht][4 + i] = (scalar)p1;
-        }
-        l_run[ht] += psum;
-      }
-    };
-
-    // QK(c+1) is issued first so its MFMAs run under the softmax of chunk c;
-    // the gather of chunk c+2 and the first V^T fragments of PV(c) go out
-    // before the softmax, which depends on neither.
-    if constexpr (MORE) qk_chunk(tile_address(c + 1));
-    if (c + 2 < chunks) fetch(c + 2);
-    v_first();
-    softmax();
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (MORE) publish(c + 1);
-
-    // PV(c): V^T fragment reads LOOK steps ahead of their MFMAs; scheduling
-    // barriers pin that distance so the registers in flight stay bounded.
-#pragma unroll
-    for (int t = 0; t < PV_STEPS; ++t) {
-      if (t + LOOK < PV_STEPS) load_step(t + LOOK);
-      const x8 v = {vlo[t][0], vlo[t][1], vlo[t][2], vlo[t][3], vhi[t][0], vhi[t][1], vhi[t][2], vhi[t][3]};
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) o[ht][t] = B16<DT>::mfma(v, pf8[ht], o[ht][t]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  // ---- 4. pipelined chunk loop ----------------------------------------------
+  // Pipeline step i: wait for KV(i), barrier, fetch KV(i+1), then the role's work.
   if (chunks > 0) {
+    if constexpr (ROW_LOADS) read_entries(0);
     fetch(0);
-    stash(0);
-    if (chunks > 1) fetch(1);
-    block_barrier();
-    qk_chunk(tile_address(0));
-    publish(0);
-    for (int c = 0; c + 1 < chunks; ++c) iteration(c, std::true_type{});
-    iteration(chunks - 1, std::false_type{});
   }
+  auto step_begin = [&](int i) {
+    if (i < chunks) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    block_barrier();
+    if (i + 1 < chunks) fetch(i + 1);
+  };
 
-  // ---- 5. normalise and store: this lane holds d = dbase + 16t + 4g + i.
+  // The swizzle only permutes units within aligned groups of 16 (256 bytes),
+  // so a fragment address is a per-lane base plus a compile-time offset.
+  if (scorer) {
+    // ---- 4a. score wave: QK, online softmax, P -------------------------------
+    // The running max (log2 units) starts at the sink and is raised (with l
+    // rescaled here and O rescaled by the output waves) only when a head's max
+    // exceeds it by more than TAU. This lane holds S^T rows sigma(4g+i) and
+    // 16 + sigma(4g+i) of head qhead.
+    float m_run = a.sinks[qhead] * LOG2E;
+    float l_run = g == 0 ? 1.0f : 0.0f;  // e^(sink - m) counted once per head
+    const float scale_log2 = a.scale * LOG2E;
+    const int ra = sigma(i16);           // KV fragment row inside a 16-row tile
+    uint32_t qk_base[4];
 #pragma unroll
-  for (int ht = 0; ht < HT; ++ht) {
-    const float inv = 1.0f / sum_over_lane_groups(l_run[ht]);
-    scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + hbase + 16 * ht) * D + dbase + 4 * g;
+    for (int b = 0; b < 4; ++b) qk_base[b] = (uint32_t)(ra * ROW_BYTES + (((4 * b + g) ^ (ra & 15)) << 4));
+
+    for (int i = 0; i <= chunks; ++i) {
+      step_begin(i);
+      if (i == chunks) break;
+      // S^T of chunk i: fragment reads LOOK_QK k-steps ahead of the MFMAs.
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      {
+        const uint32_t tile = tile_address(i);
+        uint32_t base[4];
 #pragma unroll
-    for (int t = 0; t < PV_STEPS; ++t) {
-      x4 v;
+        for (int b = 0; b < 4; ++b) base[b] = opaque(tile + qk_base[b]);
+        x8 ka0[QK_STEPS], ka1[QK_STEPS];
+        auto load = [&](int j) {
+          const AFA_LDS uint8_t* q = lds_at<uint8_t>(base[j & 3]) + (j >> 2) * 256;
+          ka0[j] = *(const AFA_LDS x8*)q;
+          ka1[j] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
+        };
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (scalar)(o[ht][t][i] * inv);
-      *(x4*)(out_row + 16 * t) = v;
+        for (int j = 0; j < LOOK_QK && j < QK_STEPS; ++j) load(j);
+        // Scheduling barriers pin the read distance: left alone, the compiler
+        // pulls every read next to its MFMA and each waits a full LDS latency.
+#pragma unroll
+        for (int j = 0; j < QK_STEPS; ++j) {
+          if (j + LOOK_QK < QK_STEPS) load(j + LOOK_QK);
+          s0 = B16<DT>::mfma(ka0[j], qf[j], s0);
+          s1 = B16<DT>::mfma(ka1[j], qf[j], s1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // Online softmax; the scale is positive, so the chunk max is taken on
+      // the raw scores and the scale goes into the exponent's FMA. Only the
+      // last chunk holds padding rows.
+      const int slot = i & 1;
+      float x0[4], x1[4];
+      float cmax = -INFINITY;
+      const int live = n_rows - i * CHUNK;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x0[k] = s0[k];
+        x1[k] = s1[k];
+        if (live < CHUNK) {
+          const int row = sigma(4 * g + k);
+          x0[k] = (row < live) ? x0[k] : -INFINITY;
+          x1[k] = (16 + row < live) ? x1[k] : -INFINITY;
+        }
+        cmax = fmaxf(cmax, fmaxf(x0[k], x1[k]));
+      }
+      cmax = max_over_lane_groups(cmax);
+      const float m_new = fmaxf(m_run, cmax * scale_log2);
+      const bool raise = __ballot(m_new > m_run + TAU) != 0ull;
+      if (raise) {
+        const float alpha = fast_exp2(m_run - m_new);
+        l_run *= alpha;
+        m_run = m_new;
+        if (g == 0) alpha_lds[slot][16 * wave + i16] = alpha;
+      }
+      if (lane == 0) flag_lds[slot][wave] = raise ? 1 : 0;
+      const float neg_m = -m_run;
+      float psum = 0.f;
+      x8 p8;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float p0 = fast_exp2(__builtin_fmaf(x0[k], scale_log2, neg_m));
+        const float p1 = fast_exp2(__builtin_fmaf(x1[k], scale_log2, neg_m));
+        psum += p0 + p1;
+        p8[k] = (scalar)p0;
+        p8[4 + k] = (scalar)p1;
+      }
+      l_run += psum;
+      p_lds[slot][wave][lane] = __builtin_bit_cast(u32x4, p8);
+    }
+    const float l = sum_over_lane_groups(l_run);
+    if (g == 0) linv_lds[16 * wave + i16] = 1.0f / l;
+    __syncthreads();
+  } else {
+    // ---- 4b. output wave: O^T[features, heads] += V^T * P^T ------------------
+    const int dbase = (wave - NQ) * DPV;
+    f32x4 o[NQ][PVT];
+#pragma unroll
+    for (int ht = 0; ht < NQ; ++ht)
+#pragma unroll
+      for (int t = 0; t < PVT; ++t) o[ht][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Transposing-read base of 16-feature tile t (t < 8; tile t + 8 is 256
+    // bytes further on when the range spans whole swizzle groups).
+    constexpr int NB = PVT < 8 ? PVT : 8;
+    const int rt = sigma(4 * g + (i16 >> 2));  // chunk row of this lane's read inside a tile
+    uint32_t tr_base[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      tr_base[b] = (uint32_t)(rt * ROW_BYTES + (((dbase / 8 + 2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
+
+    for (int i = 0; i <= chunks; ++i) {
+      step_begin(i);
+      if (i == 0) continue;
+      const int c = i - 1, slot = c & 1;
+      // Rescale flags, P and the first V^T fragments go out together; the
+      // flags are waited on first.
+      const u32x4 flags = *lds_at<u32x4>(lds_address(flag_lds[slot]));
+      x8 pb[NQ];
+#pragma unroll
+      for (int ht = 0; ht < NQ; ++ht) pb[ht] = __builtin_bit_cast(x8, p_lds[slot][ht][lane]);
+      const uint32_t tile = tile_address(c);
+      uint32_t vbase[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) vbase[b] = opaque(tile + tr_base[b]);
+      x4 vlo[PVT], vhi[PVT];
+      auto load_step = [&](int t) {
+        const AFA_LDS uint8_t* p = lds_at<uint8_t>(vbase[t % NB]) + (t / NB) * 256;
+        vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
+        vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
+      };
+#pragma unroll
+      for (int t = 0; t < LOOK && t < PVT; ++t) load_step(t);
+      // Apply the rescale factors of heads whose running max was raised.
+#pragma unroll
+      for (int ht = 0; ht < NQ; ++ht) {
+        if (__builtin_amdgcn_readfirstlane(flags[ht])) {
+          const float alpha = alpha_lds[slot][16 * ht + i16];
+#pragma unroll
+          for (int t = 0; t < PVT; ++t) o[ht][t] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < PVT; ++t) {
+        if (t + LOOK < PVT) load_step(t + LOOK);
+        const x8 v = {vlo[t][0], vlo[t][1], vlo[t][2], vlo[t][3], vhi[t][0], vhi[t][1], vhi[t][2], vhi[t][3]};
+#pragma unroll
+        for (int ht = 0; ht < NQ; ++ht) o[ht][t] = B16<DT>::mfma(v, pb[ht], o[ht][t]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();
+    // ---- 5. normalise and store: this lane holds head head0 + 16ht + i16,
+    // features dbase + 16t + 4g + i.
+#pragma unroll
+    for (int ht = 0; ht < NQ; ++ht) {
+      const float inv = linv_lds[16 * ht + i16];
+      scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + 16 * ht + i16) * D + dbase + 4 * g;
+#pragma unroll
+      for (int t = 0; t < PVT; ++t) {
+        x4 v;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
+        *(x4*)(out_row + 16 * t) = v;
+      }
     }
   }
 }
@@ -596,24 +588,24 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   return a;
 }
 
-template <int DT, int D, int HG, int HT, int DS>
+template <int DT, int D, int NQ, int NP>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   const int list = (a.WINDOW + a.TOPK + CHUNK - 1) / CHUNK * CHUNK;
   const size_t lds = (size_t)list * sizeof(uint32_t);
   const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
-  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, HG, HT, DS>), dim3(blocks), dim3(HG * DS * 64),
-                     lds, stream, a);
+  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   return (int)hipGetLastError();
 }
 
-// BM = 16 * HG * HT heads per workgroup.
+// BM = 16 * NQ heads per workgroup: 4 score + 4 output waves for BM = 64,
+// 2 + 2 for BM = 32.
 template <int DT>
 static int dispatch_d(const SparseArgs& a, hipStream_t s) {
   const bool four = a.BM == 64;
   switch (a.D) {
-    case 128: return four ? launch_fused<DT, 128, 2, 2, 1>(a, s) : launch_fused<DT, 128, 1, 2, 1>(a, s);
-    case 256: return four ? launch_fused<DT, 256, 2, 2, 2>(a, s) : launch_fused<DT, 256, 1, 2, 2>(a, s);
-    default: return four ? launch_fused<DT, 512, 4, 1, 2>(a, s) : launch_fused<DT, 512, 2, 1, 2>(a, s);
+    case 128: return four ? launch_fused<DT, 128, 4, 4>(a, s) : launch_fused<DT, 128, 2, 2>(a, s);
+    case 256: return four ? launch_fused<DT, 256, 4, 4>(a, s) : launch_fused<DT, 256, 2, 2>(a, s);
+    default: return four ? launch_fused<DT, 512, 4, 4>(a, s) : launch_fused<DT, 512, 2, 2>(a, s);
   }
 }
 
