@@ -77,24 +77,6 @@ __device__ __forceinline__ int request_by_search(const SparseArgs& a, int token)
   return lo;
 }
 
-// The same request for a whole workgroup with one round of parallel loads:
-// since cu is non-decreasing and cu[0] = 0 <= token, the answer is
-// #{b in [0, B): cu[b] <= token} - 1.
-template <int NW>
-__device__ __forceinline__ int request_by_count(const SparseArgs& a, int token, int* scratch) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  int n = 0;
-  for (int b = tid; b < a.B; b += NW * 64) n += a.cu[b] <= token ? 1 : 0;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) n += __shfl_xor(n, d);
-  if (lane == 0) scratch[wave] = n;
-  __syncthreads();
-  int total = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) total += scratch[w];
-  return total - 1;
-}
-
 // query_metadata (gather.py:8-35) and the compressed bound (attention.py:339-341)
 // of a token whose request is `batch`.
 __device__ __forceinline__ Geometry token_geometry(const SparseArgs& a, int token, int batch) {
@@ -214,7 +196,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   __shared__ float alpha_lds[2][BMH];   // O rescale factor per head, valid when flagged
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];  // score wave q raised its running max
   __shared__ float linv_lds[BMH];       // 1 / softmax denominator per head
-  __shared__ int wave_count[NW];
+  __shared__ int wave_count[2][NW];
   extern __shared__ __attribute__((aligned(16))) uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
   const int tid = threadIdx.x;
@@ -228,8 +210,9 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   const int token = (int)(logical / head_tiles);
   const int head0 = (int)(logical % head_tiles) * a.BM;
 
-  // ---- 1. Q fragments of a score wave (B operand of S^T = KV * Q^T), issued
-  // first so their latency overlaps the request search and the row list.
+  // ---- 1. loads that depend only on the token, issued together: Q fragments
+  // of a score wave (B operand of S^T = KV * Q^T), the request count and the
+  // compressed indices of the first GP passes of slots.
   const int qhead = head0 + 16 * wave + i16;   // score wave: this lane's head
   x8 qf[QK_STEPS];
   if (scorer) {
@@ -237,32 +220,93 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
 #pragma unroll
     for (int j = 0; j < QK_STEPS; ++j) qf[j] = *(const x8*)(q_row + 32 * j);
   }
-
-  __shared__ int request_scratch[NW];
-  const Geometry geo = token_geometry(a, token, request_by_count<NW>(a, token, request_scratch));
-
-  // ---- 2. compact the selected rows into the LDS row list -------------------
-  const int slots = a.WINDOW + geo.count_cmp;
-  int n_rows = 0;
-  for (int s0 = 0; s0 < slots; s0 += NT) {
-    const int s = s0 + tid;
-    uint32_t entry = 0;
-    const bool valid = s < slots && resolve_slot(a, geo, token, s, entry);
-    const uint64_t mask = __ballot(valid);
-    if (lane == 0) wave_count[wave] = __popcll(mask);
-    __syncthreads();
-    int before = 0, total = 0;
+  // Request of the token: cu is non-decreasing with cu[0] = 0 <= token, so it
+  // is #{b in [0, B): cu[b] <= token} - 1 (gather.py:10-21; empty requests
+  // have cu[b] == cu[b+1] and are skipped).
+  int below = 0;
+  for (int b = tid; b < a.B; b += NT) below += a.cu[b] <= token ? 1 : 0;
+  constexpr int GP = 2;  // passes of NT slots resolved together
+  int index[GP];
+  auto load_indices = [&](int s0) {
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int c = wave_count[w];
-      before += w < wave ? c : 0;
-      total += c;
+    for (int k = 0; k < GP; ++k) {
+      const int rank = s0 + k * NT + tid - a.WINDOW;
+      index[k] = (rank >= 0 && rank < a.TOPK) ? a.indices[(size_t)token * a.TOPK + rank] : -1;
     }
-    if (valid) {
-      const int within = __popcll(mask & ((1ull << lane) - 1ull));
-      row_list[n_rows + before + within] = entry;
+  };
+  load_indices(0);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) below += __shfl_xor(below, d);
+  __shared__ int request_scratch[NW];
+  if (lane == 0) request_scratch[wave] = below;
+  __syncthreads();
+  int requests = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) requests += request_scratch[w];
+  const int batch = requests - 1;
+
+  // ---- 2. geometry and page-table lookups; compact the selected rows -------
+  // The compressed page lookups need only the request and the indices, so
+  // they go out with the geometry loads; the window lookups need the geometry.
+  const int cpage = a.PAGE / a.RATIO;
+  const int* cmp_row = a.cmp_table + (size_t)batch * a.table_width;
+  const int* ori_row = a.ori_table + (size_t)batch * a.table_width;
+  int cblock[GP];
+  auto load_cmp_blocks = [&]() {
+#pragma unroll
+    for (int k = 0; k < GP; ++k)
+      cblock[k] = index[k] >= 0 ? cmp_row[min(index[k] / cpage, a.table_width - 1)] : -1;
+  };
+  load_cmp_blocks();
+  const Geometry geo = token_geometry(a, token, batch);
+  const int slots = a.WINDOW + geo.count_cmp;
+  // Slot s (window slot s < WINDOW, else compressed rank s - WINDOW) resolves
+  // to a tagged physical row as in resolve_slot (gather.py:38-60, 116-127).
+  int n_rows = 0;
+  for (int s0 = 0; s0 < slots; s0 += GP * NT) {
+    if (s0 > 0) {
+      load_indices(s0);
+      load_cmp_blocks();
     }
-    n_rows += total;
+    uint32_t entry[GP];
+    bool valid[GP];
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      const int s = s0 + k * NT + tid;
+      valid[k] = false;
+      entry[k] = 0;
+      if (s < a.WINDOW) {
+        if (s < geo.visible) {
+          const int position = geo.right - geo.visible + s;
+          const int block = ori_row[min(position / a.PAGE, a.table_width - 1)];
+          valid[k] = block >= 0 && block < a.ori_blocks;
+          entry[k] = (uint32_t)(block * a.PAGE + position % a.PAGE);
+        }
+      } else if (s < slots) {
+        valid[k] = index[k] >= 0 && index[k] < geo.cutoff && cblock[k] >= 0 && cblock[k] < a.cmp_blocks;
+        entry[k] = CMP_BIT | (uint32_t)(cblock[k] * cpage + index[k] % cpage);
+      }
+    }
+    // Order-preserving compaction of the GP passes, one pair of barriers.
+    uint64_t mask[GP];
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      mask[k] = __ballot(valid[k]);
+      if (lane == 0) wave_count[k][wave] = __popcll(mask[k]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      int before = 0, total = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const int c = wave_count[k][w];
+        before += w < wave ? c : 0;
+        total += c;
+      }
+      if (valid[k]) row_list[n_rows + before + __popcll(mask[k] & ((1ull << lane) - 1ull))] = entry[k];
+      n_rows += total;
+    }
     __syncthreads();
   }
   // Pad the last chunk with a real row so every load is unconditional; the
@@ -271,11 +315,11 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   if (tid < chunks * CHUNK - n_rows) row_list[n_rows + tid] = row_list[0];
   if (a.debug_rows != nullptr && head0 == 0) {
     for (int s = tid; s < a.S; s += NT) {
-      uint32_t entry = 0;
-      const bool valid = s < slots && resolve_slot(a, geo, token, s, entry);
-      int2 v = make_int2(-1, -1);
-      if (valid) v = make_int2((entry & CMP_BIT) ? 1 : 0, (int)(entry & ~CMP_BIT));
-      ((int2*)a.debug_rows)[(size_t)token * a.S + s] = v;
+      uint32_t e = 0;
+      const bool v = s < slots && resolve_slot(a, geo, token, s, e);
+      int2 r = make_int2(-1, -1);
+      if (v) r = make_int2((e & CMP_BIT) ? 1 : 0, (int)(e & ~CMP_BIT));
+      ((int2*)a.debug_rows)[(size_t)token * a.S + s] = r;
     }
   }
   __syncthreads();
