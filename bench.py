@@ -59,14 +59,18 @@ def time_launches(launch, steps, warmup, flush):
     return statistics.median(ms), ms, wall
 
 
-def warm_clocks(launch, seconds=1.0):
+def warm_clocks(launch, flush, seconds=1.0):
     """Run the first workload for about `seconds` before any timing: the GPU
-    otherwise reports its first launches at ramping clocks (about 10% slower)."""
+    otherwise reports its first launches at ramping clocks (about 10% slower).
+    Each launch is preceded by the same cache flush as a timed launch, so every
+    dispatch of the kernel in a profile of this process runs under the timed
+    conditions and the profile's average duration matches the timed median."""
     import torch
 
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         for _ in range(20):
+            flush()
             launch()
         torch.cuda.synchronize()
 
@@ -84,7 +88,7 @@ def sparse_config(name, batch, queries, context, steps, warmup, flush, device, p
     log(f"[bench] {name}: inputs ready in {time.perf_counter() - t0:.1f}s")
     args, kwargs = inputs.call_args(), inputs.call_kwargs()
     if prewarm:
-        warm_clocks(lambda: sparse_mla(*args, **kwargs), prewarm)
+        warm_clocks(lambda: sparse_mla(*args, **kwargs), flush, prewarm)
     median, samples, wall = time_launches(lambda: sparse_mla(*args, **kwargs), steps, warmup, flush)
     flops = effective_flops(policy, inputs.host, context)
     nbytes = compulsory_bytes(policy, inputs.touched)

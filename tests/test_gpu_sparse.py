@@ -23,6 +23,9 @@ VARIANTS = {
     "bf16-d512-bm32-r2": dict(DTYPE="bf16", D=512, H=64, BM=32, RATIO=2),
     "f16-d256-bm64-r1": dict(DTYPE="f16", D=256, H=64, BM=64, RATIO=1),
     "bf16-d128-bm32-r2": dict(DTYPE="bf16", D=128, H=32, BM=32, RATIO=2),
+    # A long selection: S = 3712, within the reference's resident capacity of
+    # 4096 (attention.py:261); the LDS row list then holds 3712 entries.
+    "bf16-d512-bm64-r2-topk3584": dict(DTYPE="bf16", D=512, H=64, BM=64, RATIO=2, TOPK=3584),
 }
 
 
@@ -77,12 +80,18 @@ def test_relaunch_is_bitwise_deterministic(device):
 
 
 def check_measured(inputs, tokens, device):
+    """Runs without the debug image first (the path the benchmark takes), then
+    with it; the debug dump must not change any output bit, for every token."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
     policy = inputs.policy
+    sparse_mla(*inputs.call_args(), **inputs.call_kwargs())
+    torch.cuda.synchronize()
+    plain = inputs.tensors["attention_out"].clone()
     debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
     sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), debug_rows=debug)
     torch.cuda.synchronize()
+    assert torch.equal(plain, inputs.tensors["attention_out"]), "the debug image changed the output"
     data = host_view(inputs, tokens)
     index = torch.as_tensor(tokens, device=device)
     np.testing.assert_array_equal(debug[index].cpu().numpy(), expected_rows(data, policy, tokens))
