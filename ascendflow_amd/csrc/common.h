@@ -120,6 +120,20 @@ __device__ __forceinline__ uint32_t opaque_uniform(uint32_t v) {
   return v;
 }
 
+// s_waitcnt immediate for lgkmcnt(0) alone (gfx9 encoding: vmcnt[3:0] |
+// expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14, all other fields at max).
+constexpr int WAIT_LGKM0 = 0xC07F;
+// Workgroup barrier without the memory fence of __syncthreads(): global loads
+// of later chunks stay in flight across it. The caller's own LDS stores are
+// complete (lgkmcnt(0)) before it signals; the empty asm statements keep the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
 // Blocks are dispatched round-robin over the 8 XCDs of an MI355X. Map the
 // hardware block id to a logical id so that each XCD receives a contiguous
 // range of logical ids (neighbouring work shares that XCD's L2).

@@ -34,29 +34,49 @@ struct FaArgs {
 };
 
 
-// KC keys per LDS stage; NW waves; QT 16-row query tiles per wave; D = 128.
-template <int DT, int D, int NW, int QT, int KC>
+// Flash-attention forward for D = 128. One workgroup of NW waves owns BQ =
+// NW * QT * 16 query rows of one (batch, head); each wave owns QT 16-row query
+// tiles with Q resident in registers. K and V stream in KC-key chunks through
+// a 3-stage LDS ring filled by the load-to-LDS path two chunks ahead (rows
+// XOR-swizzled on the global side, unit u of row r at u ^ (r & 15)).
+// S^T[keys, queries] = K * Q^T and O^T[d, queries] += V^T * P^T run on
+// v_mfma_f32_16x16x32_{f16,bf16}; V^T fragments come through
+// ds_read_b64_tr_b16. Per chunk c the QK MFMAs of chunk c + 1 are issued
+// ahead of the softmax of chunk c, so they run under its VALU work.
+//
+// Online softmax (attention.py:73-139) in FP32 registers, exp2 domain: the
+// chunk max is taken on raw scores (the scale is positive) and the scale goes
+// into the exponent's FMA; the running max is raised, with O and l rescaled
+// by alpha = 2^(m - m'), only when some query's max exceeds it by more than
+// FA_TAU, so P <= 2^FA_TAU; O / l is independent of the reference point.
+// Masks (attention.py:96-110): keys >= Sk, and for causal attention key j is
+// visible to query i iff j <= i (top-left); they are applied only in chunks
+// that reach the tail or the diagonal.
+constexpr float FA_TAU = 8.0f;
+constexpr int FA_NSTAGE = 3;
+
+template <int DT, int NW, int QT>
 __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
   typedef typename B16<DT>::x4 x4;
-  constexpr int NT = NW * 64;
-  constexpr int UNITS = D / 8;
-  constexpr int ROW_BYTES = D * 2;
-  constexpr int PIECES = KC * UNITS / NT;  // per tensor (K and V) per thread
-  constexpr int KT = KC / 16;              // key tiles per chunk
-  constexpr int BQ = NW * QT * 16;         // query rows per workgroup
-  static_assert(KC * UNITS % NT == 0, "chunk must split evenly");
-  static_assert(KC % 32 == 0, "chunk must hold whole PV k-steps");
+  constexpr int D = 128, ROW_BYTES = 2 * D, UNITS = D / 8;
+  constexpr int KC = 64;                       // keys per chunk
+  constexpr int KT = KC / 16;                  // key tiles per chunk
+  constexpr int TILE = KC * ROW_BYTES;         // bytes of one K or V tile
+  constexpr int BQ = NW * QT * 16;
+  constexpr int ROWS_PER_LOAD = 64 / UNITS;    // rows one wave load covers
+  constexpr int LOADS = KC / ROWS_PER_LOAD / NW;  // wave loads per tensor per chunk
+  static_assert(LOADS * ROWS_PER_LOAD * NW == KC, "a chunk must split evenly over the waves");
 
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[2][KC * ROW_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[2][KC * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[FA_NSTAGE][2][TILE];  // [stage][K, V]
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int g = lane >> 4, i16 = lane & 15;
   const int64_t q_tiles = (a.Sq + BQ - 1) / BQ;
   const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
-  // Causal: give the longest tiles (largest query rows) the lowest ids.
+  // Causal: the longest tiles (largest query rows) get the lowest ids.
   int64_t qtile = (int64_t)(logical % q_tiles);
   if (a.causal) qtile = q_tiles - 1 - qtile;
   const int64_t bh = logical / q_tiles;
@@ -65,98 +85,139 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
   const int64_t q0 = qtile * BQ;
 
   const scalar* Q = (const scalar*)a.q + ((int64_t)batch * a.HQ + head) * a.Sq * D;
-  const scalar* K = (const scalar*)a.k + ((int64_t)batch * a.HKV + kv_head) * a.Sk * D;
-  const scalar* V = (const scalar*)a.v + ((int64_t)batch * a.HKV + kv_head) * a.Sk * D;
+  const char* K = (const char*)a.k + ((int64_t)batch * a.HKV + kv_head) * a.Sk * ROW_BYTES;
+  const char* V = (const char*)a.v + ((int64_t)batch * a.HKV + kv_head) * a.Sk * ROW_BYTES;
   scalar* O = (scalar*)a.o + ((int64_t)batch * a.HQ + head) * a.Sq * D;
 
-  // Q fragments: B operand of S^T = K * Q^T. Query row of tile qt: q0 + wave*QT*16 + qt*16 + i16.
+  // Q fragments: B operand of S^T = K * Q^T; query of tile qt: q0 + (wave*QT + qt)*16 + i16.
   x8 qf[QT][D / 32];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int64_t row = q0 + (wave * QT + qt) * 16 + i16;
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j) {
-      if (row < a.Sq) {
-        qf[qt][j] = *(const x8*)(Q + row * D + 32 * j + 8 * g);
-      } else {
-        qf[qt][j] = __builtin_bit_cast(x8, u32x4{0u, 0u, 0u, 0u});
-      }
-    }
+    for (int j = 0; j < D / 32; ++j)
+      qf[qt][j] = row < a.Sq ? *(const x8*)(Q + row * D + 32 * j + 8 * g) : __builtin_bit_cast(x8, u32x4{0u, 0u, 0u, 0u});
   }
+
+  int64_t kv_end = a.Sk;
+  if (a.causal) kv_end = min(a.Sk, q0 + BQ);  // keys past the tile's last query are masked
+  const int chunks = (int)((kv_end + KC - 1) / KC);
+  // First chunk that needs masking: it reaches Sk or (causal) the tile's first query.
+  int64_t clean_end = a.Sk;
+  if (a.causal) clean_end = min(clean_end, q0 + 1);
+  const int clean_chunks = (int)(clean_end / KC);
+
+  // ---- KV movement ---------------------------------------------------------
+  const uint32_t kv_base = lds_address(kv_lds[0][0]);
+  auto tile_address = [&](int chunk, int tensor) {
+    return opaque_uniform(kv_base + (uint32_t)((chunk % FA_NSTAGE) * 2 + tensor) * TILE);
+  };
+  // Wave load p of a chunk covers rows [(wave*LOADS + p)*ROWS_PER_LOAD, +ROWS_PER_LOAD);
+  // this lane lands on unit (lane % UNITS) of row lane / UNITS and loads unit
+  // (lane % UNITS) ^ (row & 15) of that row.
+  uint32_t load_offset[LOADS];
+#pragma unroll
+  for (int p = 0; p < LOADS; ++p) {
+    const int r = (wave * LOADS + p) * ROWS_PER_LOAD + lane / UNITS;
+    load_offset[p] = (uint32_t)(r * ROW_BYTES + (((lane % UNITS) ^ (r & 15)) << 4));
+  }
+  auto fetch = [&](int chunk) {
+    const int64_t key0 = (int64_t)chunk * KC;
+    const char* kbase = K + key0 * ROW_BYTES;
+    const char* vbase = V + key0 * ROW_BYTES;
+    const bool tail = key0 + KC > a.Sk;
+#pragma unroll
+    for (int p = 0; p < LOADS; ++p) {
+      uint32_t off = load_offset[p];
+      if (tail) {  // rows past Sk read the last key instead (masked later)
+        const int r = (wave * LOADS + p) * ROWS_PER_LOAD + lane / UNITS;
+        const int rr = (int)min((int64_t)r, a.Sk - 1 - key0);
+        off = (uint32_t)(rr * ROW_BYTES + (((lane % UNITS) ^ (r & 15)) << 4));
+      }
+      const uint32_t row0 = (uint32_t)((wave * LOADS + p) * ROWS_PER_LOAD * ROW_BYTES);
+      const uint32_t kd = tile_address(chunk, 0) + row0, vd = tile_address(chunk, 1) + row0;
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                       :: "s"(kd), "v"(off), "s"(kbase) : "memory");
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                       :: "s"(vd), "v"(off), "s"(vbase) : "memory");
+    }
+  };
+
+  // ---- fragment addressing ---------------------------------------------------
+  const int ra = sigma(i16);                 // K fragment row inside a 16-key tile
+  const int rt = sigma(4 * g + (i16 >> 2));  // transposing-read row inside a tile
+  uint32_t qk_base[D / 32], tr_base[D / 16];
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) qk_base[j] = (uint32_t)(ra * ROW_BYTES + (((4 * j + g) ^ (ra & 15)) << 4));
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+    tr_base[t] = (uint32_t)(rt * ROW_BYTES + (((2 * t + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
+
   f32x4 o[QT][D / 16];
   float m_run[QT], l_run[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -INFINITY;
+    m_run[qt] = -1e30f;  // finite: a fully masked chunk then gives p = 0, never NaN
     l_run[qt] = 0.f;
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) o[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const float scale_log2 = a.scale * FA_LOG2E;
 
-  int64_t kv_end = a.Sk;
-  if (a.causal) kv_end = min(a.Sk, q0 + BQ);  // keys beyond the tile's last query are masked
-  const int chunks = (int)((kv_end + KC - 1) / KC);
-
-  u32x4 pk[PIECES], pv[PIECES];
-  auto fetch = [&](int chunk) {
+  // S^T of one chunk: K fragments LOOK steps ahead of their MFMAs.
+  constexpr int QK_FRAGS = (D / 32) * KT;  // 16 fragments, each feeds QT MFMAs
+  constexpr int LOOK = 6;
+  auto qk_chunk = [&](int chunk, f32x4 (&s)[KT][QT]) {
+    const uint32_t tile = tile_address(chunk, 0);
+    uint32_t base[D / 32];
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int flat = tid + p * NT, r = flat / UNITS, u = flat % UNITS;
-      const int64_t key = (int64_t)chunk * KC + r;
-      if (key < a.Sk) {
-        pk[p] = *(const u32x4*)(K + key * D + u * 8);
-        pv[p] = *(const u32x4*)(V + key * D + u * 8);
-      } else {
-        pk[p] = u32x4{0u, 0u, 0u, 0u};
-        pv[p] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < PIECES; ++p) {
-      const int flat = tid + p * NT, r = flat / UNITS, u = flat % UNITS;
-      const int off = r * ROW_BYTES + (swz(r, u) << 4);
-      *(u32x4*)(&k_lds[buf][off]) = pk[p];
-      *(u32x4*)(&v_lds[buf][off]) = pv[p];
-    }
-  };
-
-  const int ra = sigma(i16);
-  const int rt = sigma(4 * g + (i16 >> 2));
-  const int tr_half = (i16 & 1) * 8, tr_unit = (i16 & 3) >> 1;
-
-  if (chunks > 0) fetch(0);
-  for (int c = 0; c < chunks; ++c) {
-    const int buf = c & 1;
-    stash(buf);
-    __syncthreads();
-    if (c + 1 < chunks) fetch(c + 1);
-    const uint8_t* kt = k_lds[buf];
-    const uint8_t* vt = v_lds[buf];
-    const int64_t key0 = (int64_t)c * KC;
-
-    // S^T[key tile kt_][query tile qt].
-    f32x4 s[KT][QT];
+    for (int j = 0; j < D / 32; ++j) base[j] = opaque(tile + qk_base[j]);
+    x8 kf[QK_FRAGS];
+    auto load = [&](int f) {  // fragment f = (j, t): k-step j, key tile t
+      const int j = f / KT, t = f % KT;
+      kf[f] = *(const AFA_LDS x8*)(lds_at<uint8_t>(base[j]) + t * 16 * ROW_BYTES);
+    };
 #pragma unroll
     for (int t = 0; t < KT; ++t)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) s[t][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j) {
-      const int u = 4 * j + g;
+    for (int f = 0; f < LOOK && f < QK_FRAGS; ++f) load(f);
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const int row = 16 * t + ra;
-        const x8 kf = *(const x8*)(kt + row * ROW_BYTES + (swz(row, u) << 4));
+    for (int f = 0; f < QK_FRAGS; ++f) {
+      if (f + LOOK < QK_FRAGS) load(f + LOOK);
+      const int j = f / KT, t = f % KT;
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) s[t][qt] = B16<DT>::mfma(kf, qf[qt][j], s[t][qt]);
-      }
+      for (int qt = 0; qt < QT; ++qt) s[t][qt] = B16<DT>::mfma(kf[f], qf[qt][j], s[t][qt]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
 
-    // Online softmax per query tile; this lane holds query q (column i16) and
-    // keys key0 + 16t + sigma(4g + i).
+  // ---- pipeline: chunk c+2 loads, QK(c+1), softmax(c), PV(c) ----------------
+  f32x4 s_cur[KT][QT], s_next[KT][QT];
+  if (chunks > 0) fetch(0);
+  if (chunks > 1) fetch(1);
+  if (chunks > 0) {
+    if (chunks > 1)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));  // KV(0) landed, KV(1) may be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    block_barrier();
+    qk_chunk(0, s_cur);
+  }
+  for (int c = 0; c < chunks; ++c) {
+    const bool more = c + 1 < chunks;
+    // KV(c+1) landed (its loads are the only ones in flight); after the
+    // barrier every wave is past PV(c-1), so tile (c+2) % 3 is free.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    block_barrier();
+    if (c + 2 < chunks) fetch(c + 2);
+    if (more) qk_chunk(c + 1, s_next);
+
+    // Online softmax of chunk c; this lane holds query (column) i16 of each
+    // query tile and keys key0 + 16t + sigma(4g + i).
+    const int64_t key0 = (int64_t)c * KC;
+    const bool masked = c >= clean_chunks;
     x8 pf[QT][KC / 32];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -167,45 +228,68 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int64_t key = key0 + 16 * t + sigma(4 * g + i);
-          const bool ok = key < a.Sk && (!a.causal || key <= query);
-          x[t][i] = ok ? s[t][qt][i] * scale_log2 : -INFINITY;
+          x[t][i] = s_cur[t][qt][i];
+          if (masked) {
+            const int64_t key = key0 + 16 * t + sigma(4 * g + i);
+            const bool ok = key < a.Sk && (!a.causal || key <= query);
+            x[t][i] = ok ? x[t][i] : -INFINITY;
+          }
           cmax = fmaxf(cmax, x[t][i]);
         }
       cmax = max_over_lane_groups(cmax);
-      const float m_new = fmaxf(m_run[qt], cmax);
-      const float base = m_new == -INFINITY ? 0.f : m_new;  // fully masked so far
-      const float alpha = fast_exp2(m_run[qt] - base);
-      m_run[qt] = m_new;
+      const float m_new = fmaxf(m_run[qt], cmax * scale_log2);
+      if (__ballot(m_new > m_run[qt] + FA_TAU) != 0ull) {
+        const float alpha = fast_exp2(m_run[qt] - m_new);
+        l_run[qt] *= alpha;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) o[qt][t] *= alpha;
+        m_run[qt] = m_new;
+      }
+      const float neg_m = -m_run[qt];
       float psum = 0.f;
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(x[t][i] - base);
+          const float p = fast_exp2(__builtin_fmaf(x[t][i], scale_log2, neg_m));
           psum += p;
           pf[qt][t >> 1][(t & 1) * 4 + i] = (scalar)p;
         }
-      l_run[qt] = l_run[qt] * alpha + psum;
-#pragma unroll
-      for (int t = 0; t < D / 16; ++t) o[qt][t] *= alpha;
+      l_run[qt] += psum;
     }
 
     // O^T[d, q] += V^T[d, keys] * P^T[keys, q].
+    {
+      const uint32_t tile = tile_address(c, 1);
+      uint32_t vb[D / 16];
 #pragma unroll
-    for (int ks = 0; ks < KC / 32; ++ks) {
+      for (int t = 0; t < D / 16; ++t) vb[t] = opaque(tile + tr_base[t]);
+      constexpr int PV_FRAGS = (KC / 32) * (D / 16);  // 16 fragments, each feeds QT MFMAs
+      constexpr int VLOOK = 3;
+      x4 vlo[PV_FRAGS], vhi[PV_FRAGS];
+      auto vload = [&](int f) {  // f = (ks, t)
+        const int ks = f / (D / 16), t = f % (D / 16);
+        const AFA_LDS uint8_t* p = lds_at<uint8_t>(vb[t]) + ks * 32 * ROW_BYTES;
+        vlo[f] = B16<DT>::read_tr((const AFA_LDS void*)p);
+        vhi[f] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
+      };
 #pragma unroll
-      for (int t = 0; t < D / 16; ++t) {
-        const int u = 2 * t + tr_unit;
-        const int r0 = 32 * ks + rt, r1 = 32 * ks + 16 + rt;
-        const x4 lo = B16<DT>::read_tr(
-            (const AFA_LDS void*)(vt + r0 * ROW_BYTES + (swz(r0, u) << 4) + tr_half));
-        const x4 hi = B16<DT>::read_tr(
-            (const AFA_LDS void*)(vt + r1 * ROW_BYTES + (swz(r1, u) << 4) + tr_half));
-        const x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      for (int f = 0; f < VLOOK; ++f) vload(f);
+#pragma unroll
+      for (int f = 0; f < PV_FRAGS; ++f) {
+        if (f + VLOOK < PV_FRAGS) vload(f + VLOOK);
+        const int ks = f / (D / 16), t = f % (D / 16);
+        const x8 vf = {vlo[f][0], vlo[f][1], vlo[f][2], vlo[f][3], vhi[f][0], vhi[f][1], vhi[f][2], vhi[f][3]};
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) o[qt][t] = B16<DT>::mfma(vf, pf[qt][ks], o[qt][t]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    }
+    if (more) {
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) s_cur[t][qt] = s_next[t][qt];
     }
   }
 
@@ -327,7 +411,7 @@ __global__ __launch_bounds__(256) void simple_attention_kernel(const _Float16* Q
 using namespace afa;
 
 namespace {
-constexpr int FA_NW = 4, FA_QT = 2, FA_KC = 64;
+constexpr int FA_NW = 8, FA_QT = 2;
 
 template <int DT>
 int launch_fa(const FaArgs& a, hipStream_t s) {
@@ -335,8 +419,7 @@ int launch_fa(const FaArgs& a, hipStream_t s) {
   const int64_t tiles = (a.Sq + BQ - 1) / BQ;
   const int64_t blocks = tiles * a.B * a.HQ;
   if (blocks > 0x7fffffffLL) return AFA_E_SHAPE;
-  hipLaunchKernelGGL((fa_forward_kernel<DT, 128, FA_NW, FA_QT, FA_KC>), dim3((unsigned)blocks),
-                     dim3(FA_NW * 64), 0, s, a);
+  hipLaunchKernelGGL((fa_forward_kernel<DT, FA_NW, FA_QT>), dim3((unsigned)blocks), dim3(FA_NW * 64), 0, s, a);
   return (int)hipGetLastError();
 }
 }  // namespace

@@ -137,20 +137,6 @@ __device__ __forceinline__ const T* row_pointer(const SparseArgs& a, uint32_t en
 // TAU, so P stays <= 2^TAU; the final O/l is independent of the reference point.
 constexpr float TAU = 8.0f;
 
-// s_waitcnt immediate for lgkmcnt(0) alone (gfx9 encoding: vmcnt[3:0] |
-// expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14, all other fields at max).
-constexpr int WAIT_LGKM0 = 0xC07F;
-// Workgroup barrier without the memory fence of __syncthreads(): global loads
-// of later chunks stay in flight across it. The caller's own LDS stores are
-// complete (lgkmcnt(0)) before it signals; the empty asm statements keep the
-// compiler from moving LDS accesses across the barrier.
-__device__ __forceinline__ void block_barrier() {
-  __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
-  __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  __asm__ volatile("" ::: "memory");
-}
-
 constexpr int NSTAGE = 3;  // KV chunk buffers in LDS
 constexpr int LOOK = 4;     // V^T fragment lookahead (16-feature tiles) of an output wave
 constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
