@@ -193,49 +193,33 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
     }
   };
 
-  // ---- pipeline: chunk c+2 loads, QK(c+1), softmax(c), PV(c) ----------------
-  f32x4 s_cur[KT][QT], s_next[KT][QT];
-  if (chunks > 0) fetch(0);
-  if (chunks > 1) fetch(1);
-  if (chunks > 0) {
-    if (chunks > 1)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));  // KV(0) landed, KV(1) may be in flight
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-    block_barrier();
-    qk_chunk(0, s_cur);
-  }
-  for (int c = 0; c < chunks; ++c) {
-    const bool more = c + 1 < chunks;
-    // KV(c+1) landed (its loads are the only ones in flight); after the
-    // barrier every wave is past PV(c-1), so tile (c+2) % 3 is free.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    block_barrier();
-    if (c + 2 < chunks) fetch(c + 2);
-    if (more) qk_chunk(c + 1, s_next);
-
-    // Online softmax of chunk c; this lane holds query (column) i16 of each
-    // query tile and keys key0 + 16t + sigma(4g + i).
-    const int64_t key0 = (int64_t)c * KC;
-    const bool masked = c >= clean_chunks;
-    x8 pf[QT][KC / 32];
+  // Online softmax of one chunk; this lane holds query (column) i16 of each
+  // query tile and keys key0 + 16t + sigma(4g + i). Masked chunks (the tail
+  // and the causal diagonal) clear the scores of keys at or past a per-column
+  // limit in one uniform branch, with 32-bit chunk-relative indices.
+  auto softmax = [&](bool masked, int64_t key0, f32x4 (&s)[KT][QT], x8 (&pf)[QT][KC / 32]) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const int64_t query = q0 + (wave * QT + qt) * 16 + i16;
       float x[KT][4];
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[t][i] = s[t][qt][i];
+      if (masked) {
+        const int64_t query = q0 + (wave * QT + qt) * 16 + i16;
+        int64_t limit = a.Sk - key0;
+        if (a.causal) limit = limit < query - key0 + 1 ? limit : query - key0 + 1;
+        const int lim = limit < 0 ? 0 : (limit > KC ? KC : (int)limit);
+#pragma unroll
+        for (int t = 0; t < KT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[t][i] = 16 * t + sigma(4 * g + i) < lim ? x[t][i] : -INFINITY;
+      }
       float cmax = -INFINITY;
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[t][i] = s_cur[t][qt][i];
-          if (masked) {
-            const int64_t key = key0 + 16 * t + sigma(4 * g + i);
-            const bool ok = key < a.Sk && (!a.causal || key <= query);
-            x[t][i] = ok ? x[t][i] : -INFINITY;
-          }
-          cmax = fmaxf(cmax, x[t][i]);
-        }
+        for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, x[t][i]);
       cmax = max_over_lane_groups(cmax);
       const float m_new = fmaxf(m_run[qt], cmax * scale_log2);
       if (__ballot(m_new > m_run[qt] + FA_TAU) != 0ull) {
@@ -257,40 +241,65 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
         }
       l_run[qt] += psum;
     }
+  };
 
-    // O^T[d, q] += V^T[d, keys] * P^T[keys, q].
-    {
-      const uint32_t tile = tile_address(c, 1);
-      uint32_t vb[D / 16];
+  // O^T[d, q] += V^T[d, keys] * P^T[keys, q].
+  auto pv_chunk = [&](int chunk, x8 (&pf)[QT][KC / 32]) {
+    const uint32_t tile = tile_address(chunk, 1);
+    uint32_t vb[D / 16];
 #pragma unroll
-      for (int t = 0; t < D / 16; ++t) vb[t] = opaque(tile + tr_base[t]);
-      constexpr int PV_FRAGS = (KC / 32) * (D / 16);  // 16 fragments, each feeds QT MFMAs
-      constexpr int VLOOK = 3;
-      x4 vlo[PV_FRAGS], vhi[PV_FRAGS];
-      auto vload = [&](int f) {  // f = (ks, t)
-        const int ks = f / (D / 16), t = f % (D / 16);
-        const AFA_LDS uint8_t* p = lds_at<uint8_t>(vb[t]) + ks * 32 * ROW_BYTES;
-        vlo[f] = B16<DT>::read_tr((const AFA_LDS void*)p);
-        vhi[f] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
-      };
+    for (int t = 0; t < D / 16; ++t) vb[t] = opaque(tile + tr_base[t]);
+    constexpr int PV_FRAGS = (KC / 32) * (D / 16);  // 16 fragments, each feeds QT MFMAs
+    constexpr int VLOOK = 3;
+    x4 vlo[PV_FRAGS], vhi[PV_FRAGS];
+    auto vload = [&](int f) {  // f = (ks, t)
+      const int ks = f / (D / 16), t = f % (D / 16);
+      const AFA_LDS uint8_t* p = lds_at<uint8_t>(vb[t]) + ks * 32 * ROW_BYTES;
+      vlo[f] = B16<DT>::read_tr((const AFA_LDS void*)p);
+      vhi[f] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
+    };
 #pragma unroll
-      for (int f = 0; f < VLOOK; ++f) vload(f);
+    for (int f = 0; f < VLOOK; ++f) vload(f);
 #pragma unroll
-      for (int f = 0; f < PV_FRAGS; ++f) {
-        if (f + VLOOK < PV_FRAGS) vload(f + VLOOK);
-        const int ks = f / (D / 16), t = f % (D / 16);
-        const x8 vf = {vlo[f][0], vlo[f][1], vlo[f][2], vlo[f][3], vhi[f][0], vhi[f][1], vhi[f][2], vhi[f][3]};
+    for (int f = 0; f < PV_FRAGS; ++f) {
+      if (f + VLOOK < PV_FRAGS) vload(f + VLOOK);
+      const int ks = f / (D / 16), t = f % (D / 16);
+      const x8 vf = {vlo[f][0], vlo[f][1], vlo[f][2], vlo[f][3], vhi[f][0], vhi[f][1], vhi[f][2], vhi[f][3]};
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) o[qt][t] = B16<DT>::mfma(vf, pf[qt][ks], o[qt][t]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int qt = 0; qt < QT; ++qt) o[qt][t] = B16<DT>::mfma(vf, pf[qt][ks], o[qt][t]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (more) {
-#pragma unroll
-      for (int t = 0; t < KT; ++t)
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) s_cur[t][qt] = s_next[t][qt];
-    }
+  };
+
+  // ---- pipeline: chunk c+2 loads, QK(c+1), softmax(c), PV(c) ----------------
+  // Chunk c's scores are in cur, QK(c+1) writes nxt; the loop is unrolled by
+  // two so the two score buffers alternate without copies.
+  f32x4 s_a[KT][QT], s_b[KT][QT];
+  if (chunks > 0) fetch(0);
+  if (chunks > 1) fetch(1);
+  if (chunks > 0) {
+    if (chunks > 1)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));  // KV(0) landed, KV(1) may be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    block_barrier();
+    qk_chunk(0, s_a);
+  }
+  auto iteration = [&](int c, f32x4 (&cur)[KT][QT], f32x4 (&nxt)[KT][QT]) {
+    // KV(c+1) landed (its loads are the only ones in flight); after the
+    // barrier every wave is past PV(c-1), so tile (c+2) % 3 is free.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    block_barrier();
+    if (c + 2 < chunks) fetch(c + 2);
+    if (c + 1 < chunks) qk_chunk(c + 1, nxt);
+    x8 pf[QT][KC / 32];
+    const int64_t key0 = (int64_t)c * KC;
+    softmax(c >= clean_chunks, key0, cur, pf);
+    pv_chunk(c, pf);
+  };
+  for (int c = 0; c < chunks; c += 2) {
+    iteration(c, s_a, s_b);
+    if (c + 1 < chunks) iteration(c + 1, s_b, s_a);
   }
 
 #pragma unroll
