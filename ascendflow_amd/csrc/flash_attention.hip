@@ -164,10 +164,12 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
   }
   const float scale_log2 = a.scale * FA_LOG2E;
 
-  // S^T of one chunk: K fragments LOOK steps ahead of their MFMAs.
+  // S^T of one chunk: K fragments LOOK steps ahead of their MFMAs. After the
+  // MFMAs of fragment f, between(f) issues independent VALU work (the softmax
+  // of the previous chunk), which runs in the shadow of the MFMA pipe.
   constexpr int QK_FRAGS = (D / 32) * KT;  // 16 fragments, each feeds QT MFMAs
   constexpr int LOOK = 6;
-  auto qk_chunk = [&](int chunk, f32x4 (&s)[KT][QT]) {
+  auto qk_chunk = [&](int chunk, f32x4 (&s)[KT][QT], auto&& between) {
     const uint32_t tile = tile_address(chunk, 0);
     uint32_t base[D / 32];
 #pragma unroll
@@ -189,67 +191,18 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       const int j = f / KT, t = f % KT;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) s[t][qt] = B16<DT>::mfma(kf[f], qf[qt][j], s[t][qt]);
+      between(f);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Online softmax of one chunk; this lane holds query (column) i16 of each
-  // query tile and keys key0 + 16t + sigma(4g + i). Masked chunks (the tail
-  // and the causal diagonal) clear the scores of keys at or past a per-column
-  // limit in one uniform branch, with 32-bit chunk-relative indices.
-  auto softmax = [&](bool masked, int64_t key0, f32x4 (&s)[KT][QT], x8 (&pf)[QT][KC / 32]) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float x[KT][4];
-#pragma unroll
-      for (int t = 0; t < KT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[t][i] = s[t][qt][i];
-      if (masked) {
-        const int64_t query = q0 + (wave * QT + qt) * 16 + i16;
-        int64_t limit = a.Sk - key0;
-        if (a.causal) limit = limit < query - key0 + 1 ? limit : query - key0 + 1;
-        const int lim = limit < 0 ? 0 : (limit > KC ? KC : (int)limit);
-#pragma unroll
-        for (int t = 0; t < KT; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) x[t][i] = 16 * t + sigma(4 * g + i) < lim ? x[t][i] : -INFINITY;
-      }
-      float cmax = -INFINITY;
-#pragma unroll
-      for (int t = 0; t < KT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cmax = fmaxf(cmax, x[t][i]);
-      cmax = max_over_lane_groups(cmax);
-      const float m_new = fmaxf(m_run[qt], cmax * scale_log2);
-      if (__ballot(m_new > m_run[qt] + FA_TAU) != 0ull) {
-        const float alpha = fast_exp2(m_run[qt] - m_new);
-        l_run[qt] *= alpha;
-#pragma unroll
-        for (int t = 0; t < D / 16; ++t) o[qt][t] *= alpha;
-        m_run[qt] = m_new;
-      }
-      const float neg_m = -m_run[qt];
-      float psum = 0.f;
-#pragma unroll
-      for (int t = 0; t < KT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(__builtin_fmaf(x[t][i], scale_log2, neg_m));
-          psum += p;
-          pf[qt][t >> 1][(t & 1) * 4 + i] = (scalar)p;
-        }
-      l_run[qt] += psum;
-    }
-  };
-
-  // O^T[d, q] += V^T[d, keys] * P^T[keys, q].
-  auto pv_chunk = [&](int chunk, x8 (&pf)[QT][KC / 32]) {
+  // O^T[d, q] += V^T[d, keys] * P^T[keys, q], with between(f) as in qk_chunk.
+  constexpr int PV_FRAGS = (KC / 32) * (D / 16);  // 16 fragments, each feeds QT MFMAs
+  auto pv_chunk = [&](int chunk, x8 (&pf)[QT][KC / 32], auto&& between) {
     const uint32_t tile = tile_address(chunk, 1);
     uint32_t vb[D / 16];
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) vb[t] = opaque(tile + tr_base[t]);
-    constexpr int PV_FRAGS = (KC / 32) * (D / 16);  // 16 fragments, each feeds QT MFMAs
     constexpr int VLOOK = 3;
     x4 vlo[PV_FRAGS], vhi[PV_FRAGS];
     auto vload = [&](int f) {  // f = (ks, t)
@@ -267,13 +220,41 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       const x8 vf = {vlo[f][0], vlo[f][1], vlo[f][2], vlo[f][3], vhi[f][0], vhi[f][1], vhi[f][2], vhi[f][3]};
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) o[qt][t] = B16<DT>::mfma(vf, pf[qt][ks], o[qt][t]);
+      between(f);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // ---- pipeline: chunk c+2 loads, QK(c+1), softmax(c), PV(c) ----------------
-  // Chunk c's scores are in cur, QK(c+1) writes nxt; the loop is unrolled by
-  // two so the two score buffers alternate without copies.
+  // Scores of keys at or past a per-column limit (the tail chunk and the
+  // causal diagonal) become -inf; 32-bit chunk-relative indices. This lane
+  // holds query (column) i16 of each query tile and keys 16t + sigma(4g + i).
+  auto mask = [&](int chunk, f32x4 (&s)[KT][QT]) {
+    const int64_t key0 = (int64_t)chunk * KC;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int64_t query = q0 + (wave * QT + qt) * 16 + i16;
+      int64_t limit = a.Sk - key0;
+      if (a.causal) limit = limit < query - key0 + 1 ? limit : query - key0 + 1;
+      const int lim = limit < 0 ? 0 : (limit > KC ? KC : (int)limit);
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[t][qt][i] = 16 * t + sigma(4 * g + i) < lim ? s[t][qt][i] : -INFINITY;
+    }
+  };
+
+  // ---- pipeline: chunk c+2 loads, QK(c+1) + softmax(c), PV(c) + softmax(c) --
+  // Chunk c's scores are in cur (masked at the top of its iteration) and
+  // QK(c+1) writes nxt; the loop is unrolled by two so the two score buffers
+  // alternate without copies. The softmax of chunk c is spread over the MFMA
+  // steps: the first QT steps of QK(c+1) take the column maxima, the next two
+  // the cross-lane reduction and the (rare, uniform) rescale, the rest the
+  // exponentials of key tiles 0-1; the first PV(c) steps, which use only
+  // those, take the exponentials of key tiles 2-3.
+  constexpr int HALF = QT * 8;                  // exponentials per key-tile pair
+  constexpr int QK_EXP0 = QT + 2;               // first QK step with exponentials
+  constexpr int PV_EXP_STEPS = PV_FRAGS / 2 - 1;  // PV steps with exponentials
+  static_assert(QK_FRAGS > QK_EXP0, "no QK step left for exponentials");
   f32x4 s_a[KT][QT], s_b[KT][QT];
   if (chunks > 0) fetch(0);
   if (chunks > 1) fetch(1);
@@ -283,7 +264,7 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
     else
       __builtin_amdgcn_s_waitcnt(0x0F70);
     block_barrier();
-    qk_chunk(0, s_a);
+    qk_chunk(0, s_a, [](int) {});
   }
   auto iteration = [&](int c, f32x4 (&cur)[KT][QT], f32x4 (&nxt)[KT][QT]) {
     // KV(c+1) landed (its loads are the only ones in flight); after the
@@ -291,11 +272,67 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
     __builtin_amdgcn_s_waitcnt(0x0F70);
     block_barrier();
     if (c + 2 < chunks) fetch(c + 2);
-    if (c + 1 < chunks) qk_chunk(c + 1, nxt);
+    if (c >= clean_chunks) mask(c, cur);
+
     x8 pf[QT][KC / 32];
-    const int64_t key0 = (int64_t)c * KC;
-    softmax(c >= clean_chunks, key0, cur, pf);
-    pv_chunk(c, pf);
+    float cmax[QT], m_new[QT], psum[QT];
+    auto exp_element = [&](int e) {  // e = (half, qt, t & 1, i)
+      const int h = e / HALF, qt = (e / 8) % QT, t = 2 * h + (e / 4) % 2, i = e % 4;
+      const float p = fast_exp2(__builtin_fmaf(cur[t][qt][i], scale_log2, -m_run[qt]));
+      psum[qt] += p;
+      pf[qt][h][(t & 1) * 4 + i] = (scalar)p;
+    };
+    auto qk_between = [&](int f) {
+      if (f < QT) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < KT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) m = fmaxf(m, cur[t][f][i]);
+        cmax[f] = m;
+      } else if (f == QT) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          m_new[qt] = fmaxf(m_run[qt], max_over_lane_groups(cmax[qt]) * scale_log2);
+          psum[qt] = 0.f;
+        }
+      } else if (f == QT + 1) {
+        bool grow = false;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) grow |= m_new[qt] > m_run[qt] + FA_TAU;
+        if (__ballot(grow) != 0ull) {
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            const float alpha = fast_exp2(m_run[qt] - m_new[qt]);
+            l_run[qt] *= alpha;
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t) o[qt][t] *= alpha;
+            m_run[qt] = m_new[qt];
+          }
+        }
+      } else {
+        // Constant trip counts: the loop unrolls before f is known.
+#pragma unroll
+        for (int e = 0; e < HALF; ++e)
+          if (QK_EXP0 + e * (QK_FRAGS - QK_EXP0) / HALF == f) exp_element(e);
+      }
+    };
+    auto pv_between = [&](int f) {
+      if (f < PV_EXP_STEPS) {
+#pragma unroll
+        for (int e = 0; e < HALF; ++e)
+          if (e * PV_EXP_STEPS / HALF == f) exp_element(HALF + e);
+      } else if (f == PV_EXP_STEPS + 1) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) l_run[qt] += psum[qt];
+      }
+    };
+
+    // The last chunk also runs a QK, over the stale tile (c + 1) % 3 (no load
+    // is in flight into it), so that the softmax has one code path; those
+    // scores are never read.
+    qk_chunk(c + 1, nxt, qk_between);
+    pv_chunk(c, pf, pv_between);
   };
   for (int c = 0; c < chunks; c += 2) {
     iteration(c, s_a, s_b);
