@@ -126,7 +126,10 @@ def profiled_traffic(key):
     return int(match.group(1)) if match else None
 
 
-def attention_extras(steps, warmup, flush, device):
+ATTENTION_KEYS = ("fa_c2", "fa_c2_causal", "simple_c1")
+
+
+def attention_extras(steps, warmup, flush, device, which=ATTENTION_KEYS, prewarm=0.0):
     """Flash attention C2 (B1 H32 D128 S8192 f16) and teaching attention C1 timings."""
     import torch
 
@@ -138,6 +141,12 @@ def attention_extras(steps, warmup, flush, device):
     q, k, v = (torch.randn((1, 32, 8192, 128), generator=gen, device=device).to(torch.float16) for _ in range(3))
     o = torch.empty_like(q)
     for causal in (False, True):
+        if ("fa_c2_causal" if causal else "fa_c2") not in which:
+            continue
+        if prewarm:
+            warm_clocks(lambda: attention_target(q, k, v, o, 8192, 8192, B=1, HQ=32, HKV=32, D=128, CAUSAL=causal),
+                        flush, prewarm)
+            prewarm = 0.0
         ms, _, _ = time_launches(lambda: attention_target(q, k, v, o, 8192, 8192, B=1, HQ=32, HKV=32, D=128, CAUSAL=causal),
                                  steps, warmup, flush)
         flops = 4 * 32 * 128 * (8192 * 8192 if not causal else 8192 * 8193 // 2)
@@ -146,6 +155,8 @@ def attention_extras(steps, warmup, flush, device):
                                                        "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
         log(f"[bench] flash attention B1 H32 S8192 D128 f16 causal={causal}: {ms:.4f} ms, {tf:.1f} TFLOPS")
     del q, k, v, o
+    if "simple_c1" not in which:
+        return out
     qs = torch.randn((8, 1024, 128), generator=gen, device=device).to(torch.float16)
     ks, vs = (torch.randn((8, 128, 128), generator=gen, device=device).to(torch.float16) for _ in range(2))
     os_ = torch.empty_like(qs)
@@ -206,8 +217,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k"], default=None,
-                        help="time one configuration only (profiling runs)")
+    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", *ATTENTION_KEYS], default=None,
+                        help="time one configuration only (profiling runs; the attention keys print a log only)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-attention", action="store_true", help="skip the flash/teaching attention extras")
     parser.add_argument("--prewarm", type=float, default=1.0,
@@ -243,6 +254,11 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] copy calibration: 3 neg passes of {args.copy_calibration} MiB")
         del src, dst
+
+    if args.only in ATTENTION_KEYS:
+        extras = attention_extras(args.steps, args.warmup, flush, device, which=(args.only,), prewarm=args.prewarm)
+        log(f"[bench] {args.only}: {json.dumps(extras[args.only])}")
+        return 0
 
     configs = {
         "prefill8k": ("sparse_mla prefill B1 Q8192 ctx32768", 1, 8192, 32768),
