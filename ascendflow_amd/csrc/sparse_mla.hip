@@ -10,7 +10,10 @@
 //   1. resolve the token's request and window/compressed bounds
 //      (gather.py:8-35, attention.py:339-341) and compact every selected row
 //      (window positions, then compressed ranks, duplicates kept) into an LDS
-//      row list of physical row ids;
+//      row list of physical row ids. With a workspace, a plan kernel does this
+//      for every token first (three dependent global round trips that would
+//      otherwise leave the CU's matrix cores idle at each token start) and the
+//      main kernel copies the token's list into LDS with one load-to-LDS pass;
 //   2. stream the listed rows through a 3-stage ring of XOR-swizzled LDS
 //      tiles of CHUNK rows with the load-to-LDS path (global_load_lds_dwordx4,
 //      one wave load per 1 KiB row when D = 512);
@@ -52,7 +55,10 @@ struct SparseArgs {
   const float* sinks;
   void* out;
   int32_t* debug_rows;
+  uint32_t* plan_rows;   // workspace: [T][list_pad] padded row lists, or null
+  int32_t* plan_count;   // workspace: [T] selected rows per token
   int32_t B, T, H, D, PAGE, RATIO, table_width, ori_blocks, cmp_blocks, WINDOW, TOPK, S, BM;
+  int32_t list_pad;      // row-list capacity: WINDOW + TOPK rounded up to 256 (whole KiB)
   float scale;
 };
 
@@ -132,6 +138,126 @@ __device__ __forceinline__ const T* row_pointer(const SparseArgs& a, uint32_t en
   return base + (size_t)(entry & ~CMP_BIT) * a.D;
 }
 
+// Resolves the selected rows of `token` into row_list (LDS) in slot order
+// (window positions, then compressed ranks) and returns their count. Every
+// one of the NTH threads of the workgroup must call it (workgroup barriers);
+// wave_count is LDS scratch of [3][NTH / 64], request_scratch of [NTH / 64].
+// Three dependent global round trips: the request count with the compressed
+// indices, then the geometry with the compressed page lookups, then the window
+// page lookups (gather.py:8-60, 116-127; attention.py:339-341).
+template <int NTH>
+__device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint32_t* row_list,
+                                            int (*wave_count)[NTH / 64], int* request_scratch,
+                                            Geometry& geo) {
+  constexpr int NWV = NTH / 64;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  // Request of the token: cu is non-decreasing with cu[0] = 0 <= token, so it
+  // is #{b in [0, B): cu[b] <= token} - 1 (gather.py:10-21; empty requests
+  // have cu[b] == cu[b+1] and are skipped).
+  int below = 0;
+  for (int b = tid; b < a.B; b += NTH) below += a.cu[b] <= token ? 1 : 0;
+  constexpr int GP = 2;  // passes of NTH slots resolved together
+  int index[GP];
+  auto load_indices = [&](int s0) {
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      const int rank = s0 + k * NTH + tid - a.WINDOW;
+      index[k] = (rank >= 0 && rank < a.TOPK) ? a.indices[(size_t)token * a.TOPK + rank] : -1;
+    }
+  };
+  load_indices(0);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) below += __shfl_xor(below, d);
+  if (lane == 0) request_scratch[wave] = below;
+  __syncthreads();
+  int requests = 0;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) requests += request_scratch[w];
+  const int batch = requests - 1;
+
+  // The compressed page lookups need only the request and the indices, so
+  // they go out with the geometry loads; the window lookups need the geometry.
+  const int cpage = a.PAGE / a.RATIO;
+  const int* cmp_row = a.cmp_table + (size_t)batch * a.table_width;
+  const int* ori_row = a.ori_table + (size_t)batch * a.table_width;
+  int cblock[GP];
+  auto load_cmp_blocks = [&]() {
+#pragma unroll
+    for (int k = 0; k < GP; ++k)
+      cblock[k] = index[k] >= 0 ? cmp_row[min(index[k] / cpage, a.table_width - 1)] : -1;
+  };
+  load_cmp_blocks();
+  geo = token_geometry(a, token, batch);
+  const int slots = a.WINDOW + geo.count_cmp;
+  // Slot s (window slot s < WINDOW, else compressed rank s - WINDOW) resolves
+  // to a tagged physical row as in resolve_slot (gather.py:38-60, 116-127).
+  int n_rows = 0;
+  for (int s0 = 0; s0 < slots; s0 += GP * NTH) {
+    if (s0 > 0) {
+      load_indices(s0);
+      load_cmp_blocks();
+    }
+    uint32_t entry[GP];
+    bool valid[GP];
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      const int s = s0 + k * NTH + tid;
+      valid[k] = false;
+      entry[k] = 0;
+      if (s < a.WINDOW) {
+        if (s < geo.visible) {
+          const int position = geo.right - geo.visible + s;
+          const int block = ori_row[min(position / a.PAGE, a.table_width - 1)];
+          valid[k] = block >= 0 && block < a.ori_blocks;
+          entry[k] = (uint32_t)(block * a.PAGE + position % a.PAGE);
+        }
+      } else if (s < slots) {
+        valid[k] = index[k] >= 0 && index[k] < geo.cutoff && cblock[k] >= 0 && cblock[k] < a.cmp_blocks;
+        entry[k] = CMP_BIT | (uint32_t)(cblock[k] * cpage + index[k] % cpage);
+      }
+    }
+    // Order-preserving compaction of the GP passes, one pair of barriers.
+    uint64_t mask[GP];
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      mask[k] = __ballot(valid[k]);
+      if (lane == 0) wave_count[k][wave] = __popcll(mask[k]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      int before = 0, total = 0;
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) {
+        const int c = wave_count[k][w];
+        before += w < wave ? c : 0;
+        total += c;
+      }
+      if (valid[k]) row_list[n_rows + before + __popcll(mask[k] & ((1ull << lane) - 1ull))] = entry[k];
+      n_rows += total;
+    }
+    __syncthreads();
+  }
+  return n_rows;
+}
+
+// Plan kernel: one workgroup per token writes the token's row list, padded
+// with its first row to a whole number of CHUNK-row chunks, and the count.
+template <int NTH>
+__global__ __launch_bounds__(NTH) void sparse_plan_kernel(SparseArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t plan_list[];
+  __shared__ int wave_count[3][NTH / 64];
+  __shared__ int request_scratch[NTH / 64];
+  const int token = blockIdx.x;
+  Geometry geo;
+  const int n = resolve_rows<NTH>(a, token, plan_list, wave_count, request_scratch, geo);
+  const int padded = (n + CHUNK - 1) / CHUNK * CHUNK;
+  uint32_t* dst = a.plan_rows + (size_t)token * a.list_pad;
+  for (int r = threadIdx.x; r < padded; r += NTH) dst[r] = plan_list[r < n ? r : 0];
+  if (threadIdx.x == 0) a.plan_count[token] = n;
+}
+
 // Lazy rescaling threshold (log2 units): the running max used for exp2 is only
 // raised, and O/l rescaled, once some head's max exceeds it by more than
 // TAU, so P stays <= 2^TAU; the final O/l is independent of the reference point.
@@ -182,7 +308,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   __shared__ float alpha_lds[2][BMH];   // O rescale factor per head, valid when flagged
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];  // score wave q raised its running max
   __shared__ float linv_lds[BMH];       // 1 / softmax denominator per head
-  __shared__ int wave_count[2][NW];
+  __shared__ int wave_count[3][NW];
   extern __shared__ __attribute__((aligned(16))) uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
   const int tid = threadIdx.x;
@@ -196,119 +322,76 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   const int token = (int)(logical / head_tiles);
   const int head0 = (int)(logical % head_tiles) * a.BM;
 
-  // ---- 1. loads that depend only on the token, issued together: Q fragments
-  // of a score wave (B operand of S^T = KV * Q^T), the request count and the
-  // compressed indices of the first GP passes of slots.
-  const int qhead = head0 + 16 * wave + i16;   // score wave: this lane's head
-  x8 qf[QK_STEPS];
-  if (scorer) {
-    const scalar* q_row = (const scalar*)a.q + ((size_t)token * a.H + qhead) * D + 8 * g;
+  // ---- 1-2. the token's row list in LDS (from the plan, or resolved here)
+  // and Q. Q (BMH contiguous rows of D features) is copied with the
+  // load-to-LDS path in coalesced 1 KiB wave loads into ring tiles 1 and 2,
+  // which stay unused until the first pipeline step, with the KV rows' unit
+  // swizzle; each score wave then reads its B-operand fragments (S^T = KV *
+  // Q^T) from there once. Loading the fragments straight into registers
+  // touches 64-byte pieces of 16 rows per wave load and stalls the issue of
+  // every other load of the workgroup for thousands of cycles.
+  const uint32_t q_lds = lds_address(kv_lds[1]);
+  constexpr int Q_LOADS = BMH * ROW_BYTES / 1024;  // 1 KiB wave loads of the Q tile
+  static_assert(BMH * ROW_BYTES <= 2 * CHUNK * ROW_BYTES, "Q tile must fit ring tiles 1 and 2");
+  auto copy_q = [&]() {
+    const char* q_src = (const char*)a.q + ((size_t)token * a.H + head0) * ROW_BYTES;
 #pragma unroll
-    for (int j = 0; j < QK_STEPS; ++j) qf[j] = *(const x8*)(q_row + 32 * j);
-  }
-  // Request of the token: cu is non-decreasing with cu[0] = 0 <= token, so it
-  // is #{b in [0, B): cu[b] <= token} - 1 (gather.py:10-21; empty requests
-  // have cu[b] == cu[b+1] and are skipped).
-  int below = 0;
-  for (int b = tid; b < a.B; b += NT) below += a.cu[b] <= token ? 1 : 0;
-  constexpr int GP = 2;  // passes of NT slots resolved together
-  int index[GP];
-  auto load_indices = [&](int s0) {
-#pragma unroll
-    for (int k = 0; k < GP; ++k) {
-      const int rank = s0 + k * NT + tid - a.WINDOW;
-      index[k] = (rank >= 0 && rank < a.TOPK) ? a.indices[(size_t)token * a.TOPK + rank] : -1;
+    for (int k0 = 0; k0 < Q_LOADS; k0 += NW) {
+      const int k = k0 + wave;
+      if (Q_LOADS % NW == 0 || k < Q_LOADS) {
+        const int pos = k * 64 + lane;  // 16-byte unit position in the tile
+        const int r = pos / UNITS, u = pos % UNITS;
+        const uint32_t off = (uint32_t)(r * ROW_BYTES + ((u ^ (r & 15)) << 4));
+        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                         :: "s"(q_lds + (uint32_t)k * 1024u), "v"(off), "s"(q_src) : "memory");
+      }
     }
   };
-  load_indices(0);
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) below += __shfl_xor(below, d);
+  constexpr int Q_LOADS_PER_WAVE = (Q_LOADS + NW - 1) / NW;
   __shared__ int request_scratch[NW];
-  if (lane == 0) request_scratch[wave] = below;
-  __syncthreads();
-  int requests = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) requests += request_scratch[w];
-  const int batch = requests - 1;
-
-  // ---- 2. geometry and page-table lookups; compact the selected rows -------
-  // The compressed page lookups need only the request and the indices, so
-  // they go out with the geometry loads; the window lookups need the geometry.
-  const int cpage = a.PAGE / a.RATIO;
-  const int* cmp_row = a.cmp_table + (size_t)batch * a.table_width;
-  const int* ori_row = a.ori_table + (size_t)batch * a.table_width;
-  int cblock[GP];
-  auto load_cmp_blocks = [&]() {
-#pragma unroll
-    for (int k = 0; k < GP; ++k)
-      cblock[k] = index[k] >= 0 ? cmp_row[min(index[k] / cpage, a.table_width - 1)] : -1;
-  };
-  load_cmp_blocks();
-  const Geometry geo = token_geometry(a, token, batch);
-  const int slots = a.WINDOW + geo.count_cmp;
-  // Slot s (window slot s < WINDOW, else compressed rank s - WINDOW) resolves
-  // to a tagged physical row as in resolve_slot (gather.py:38-60, 116-127).
-  int n_rows = 0;
-  for (int s0 = 0; s0 < slots; s0 += GP * NT) {
-    if (s0 > 0) {
-      load_indices(s0);
-      load_cmp_blocks();
-    }
-    uint32_t entry[GP];
-    bool valid[GP];
-#pragma unroll
-    for (int k = 0; k < GP; ++k) {
-      const int s = s0 + k * NT + tid;
-      valid[k] = false;
-      entry[k] = 0;
-      if (s < a.WINDOW) {
-        if (s < geo.visible) {
-          const int position = geo.right - geo.visible + s;
-          const int block = ori_row[min(position / a.PAGE, a.table_width - 1)];
-          valid[k] = block >= 0 && block < a.ori_blocks;
-          entry[k] = (uint32_t)(block * a.PAGE + position % a.PAGE);
-        }
-      } else if (s < slots) {
-        valid[k] = index[k] >= 0 && index[k] < geo.cutoff && cblock[k] >= 0 && cblock[k] < a.cmp_blocks;
-        entry[k] = CMP_BIT | (uint32_t)(cblock[k] * cpage + index[k] % cpage);
+  int n_rows;
+  if (a.plan_rows != nullptr) {
+    // Output waves copy the count and the padded list (whole KiB units) first;
+    // every wave then copies its share of Q. The list is waited for with the
+    // Q loads still in flight.
+    if (!scorer) {
+      const uint32_t* src = a.plan_rows + (size_t)token * a.list_pad;
+      const uint32_t list_base = lds_address(row_list);
+      if (wave == NQ && lane == 0)
+        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+                         :: "s"(lds_address(request_scratch)), "v"(0u), "s"(a.plan_count + token) : "memory");
+      for (int u = wave - NQ; u < a.list_pad / 256; u += NP) {
+        const uint32_t dst = list_base + (uint32_t)u * 1024u;
+        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                         :: "s"(dst), "v"((uint32_t)lane * 16u), "s"(src + u * 256) : "memory");
       }
     }
-    // Order-preserving compaction of the GP passes, one pair of barriers.
-    uint64_t mask[GP];
-#pragma unroll
-    for (int k = 0; k < GP; ++k) {
-      mask[k] = __ballot(valid[k]);
-      if (lane == 0) wave_count[k][wave] = __popcll(mask[k]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < GP; ++k) {
-      int before = 0, total = 0;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const int c = wave_count[k][w];
-        before += w < wave ? c : 0;
-        total += c;
+    copy_q();
+    if (!scorer)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (Q_LOADS_PER_WAVE & 15) | ((Q_LOADS_PER_WAVE >> 4) << 14));
+    block_barrier();
+    n_rows = request_scratch[0];
+  } else {
+    Geometry geo;
+    n_rows = resolve_rows<NT>(a, token, row_list, wave_count, request_scratch, geo);
+    // Pad the last chunk with a real row so every load is unconditional; the
+    // padded rows get -inf scores (P = 0) below.
+    const int padded = (n_rows + CHUNK - 1) / CHUNK * CHUNK;
+    if (tid < padded - n_rows) row_list[n_rows + tid] = row_list[0];
+    if (a.debug_rows != nullptr && head0 == 0) {
+      const int slots = a.WINDOW + geo.count_cmp;
+      for (int s = tid; s < a.S; s += NT) {
+        uint32_t e = 0;
+        const bool v = s < slots && resolve_slot(a, geo, token, s, e);
+        int2 r = make_int2(-1, -1);
+        if (v) r = make_int2((e & CMP_BIT) ? 1 : 0, (int)(e & ~CMP_BIT));
+        ((int2*)a.debug_rows)[(size_t)token * a.S + s] = r;
       }
-      if (valid[k]) row_list[n_rows + before + __popcll(mask[k] & ((1ull << lane) - 1ull))] = entry[k];
-      n_rows += total;
     }
-    __syncthreads();
+    copy_q();
+    block_barrier();
   }
-  // Pad the last chunk with a real row so every load is unconditional; the
-  // padded rows get -inf scores (P = 0) below.
   const int chunks = (n_rows + CHUNK - 1) / CHUNK;
-  if (tid < chunks * CHUNK - n_rows) row_list[n_rows + tid] = row_list[0];
-  if (a.debug_rows != nullptr && head0 == 0) {
-    for (int s = tid; s < a.S; s += NT) {
-      uint32_t e = 0;
-      const bool v = s < slots && resolve_slot(a, geo, token, s, e);
-      int2 r = make_int2(-1, -1);
-      if (v) r = make_int2((e & CMP_BIT) ? 1 : 0, (int)(e & ~CMP_BIT));
-      ((int2*)a.debug_rows)[(size_t)token * a.S + s] = r;
-    }
-  }
-  __syncthreads();
 
   // ---- 3. KV movement: global -> LDS through the load-to-LDS path ------------
   // global_load_lds_dwordx4 writes one wave's 64 x 16 bytes contiguously at the
@@ -366,6 +449,22 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   if (chunks > 0) {
     if constexpr (ROW_LOADS) read_entries(0);
     fetch(0);
+    // Q has landed once at most the PIECES loads of fetch(0) are in flight.
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  }
+  block_barrier();
+  // Score wave fragments: this lane holds head 16 * wave + i16 (tile row r),
+  // features 32j + 8g .. +7, i.e. unit 4j + g of row r, stored at unit
+  // (4j + g) ^ (r & 15). Tile 1 is overwritten only after the next barrier.
+  const int qhead = head0 + 16 * wave + i16;   // score wave: this lane's head
+  x8 qf[QK_STEPS];
+  if (scorer) {
+    const int r = 16 * wave + i16;
+#pragma unroll
+    for (int j = 0; j < QK_STEPS; ++j)
+      qf[j] = *lds_at<x8>(q_lds + (uint32_t)(r * ROW_BYTES + (((4 * j + g) ^ (r & 15)) << 4)));
   }
   auto step_begin = [&](int i) {
     if (i < chunks) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -614,14 +713,43 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   a.TOPK = p->TOPK;
   a.S = p->S;
   a.BM = p->BM;
+  a.list_pad = (p->WINDOW + p->TOPK + 255) / 256 * 256;
+  a.plan_rows = nullptr;
+  a.plan_count = nullptr;
   a.scale = p->scale;
   return a;
 }
 
+// Plan workspace: [T] counts (rounded up to 256 bytes), then [T][list_pad]
+// row lists.
+static size_t plan_count_bytes(int64_t T) { return (size_t)((T * 4 + 255) / 256 * 256); }
+static size_t plan_bytes(const SparseMlaParams* p) {
+  const int64_t list_pad = (p->WINDOW + p->TOPK + 255) / 256 * 256;
+  return plan_count_bytes(p->T) + (size_t)p->T * (size_t)list_pad * 4;
+}
+
+// LDS of one workgroup (the KV ring, P slots and the row list) must fit the
+// 160 KiB a gfx950 CU holds.
+constexpr size_t LDS_BYTES = 160 * 1024;
+template <typename K>
+static int fits_lds(K kernel, size_t dynamic_bytes) {
+  hipFuncAttributes attr;
+  const hipError_t e = hipFuncGetAttributes(&attr, (const void*)kernel);
+  if (e != hipSuccess) return (int)e;
+  return attr.sharedSizeBytes + dynamic_bytes <= LDS_BYTES ? AFA_OK : AFA_E_SHAPE;
+}
+
 template <int DT, int D, int NQ, int NP>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
-  const int list = (a.WINDOW + a.TOPK + CHUNK - 1) / CHUNK * CHUNK;
-  const size_t lds = (size_t)list * sizeof(uint32_t);
+  const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
+  const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
+  if (fit) return fit;
+  if (a.plan_rows != nullptr) {
+    constexpr int PLAN_THREADS = 256;
+    hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
   const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
   hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   return (int)hipGetLastError();
@@ -647,16 +775,21 @@ extern "C" int launch_sparse_mla(void* stream, const void* q, const void* ori_kv
                                  const int32_t* ori_topk_length, const float* sinks,
                                  void* attention_out, void* workspace,
                                  const SparseMlaParams* params) {
-  (void)workspace;
   const int status = check_sparse(params);
   if (status) return status;
   if (!q || !ori_kv || !cmp_kv || !cmp_sparse_indices || !ori_block_table || !cmp_block_table ||
       !cu_seqlens_q || !seqused_ori_kv || !seqused_cmp_kv || !cmp_residual_kv ||
       !ori_topk_length || !sinks || !attention_out)
     return AFA_E_NULL;
-  const SparseArgs a = make_args(params, q, ori_kv, cmp_kv, cmp_sparse_indices, ori_block_table,
-                                 cmp_block_table, cu_seqlens_q, seqused_ori_kv, seqused_cmp_kv,
-                                 cmp_residual_kv, ori_topk_length, sinks, attention_out);
+  SparseArgs a = make_args(params, q, ori_kv, cmp_kv, cmp_sparse_indices, ori_block_table,
+                           cmp_block_table, cu_seqlens_q, seqused_ori_kv, seqused_cmp_kv,
+                           cmp_residual_kv, ori_topk_length, sinks, attention_out);
+  // With a workspace the row lists come from the plan kernel; the debug image
+  // is written by the fused setup, so a debug call resolves rows in place.
+  if (workspace != nullptr && params->debug_rows == nullptr) {
+    a.plan_count = (int32_t*)workspace;
+    a.plan_rows = (uint32_t*)((char*)workspace + plan_count_bytes(params->T));
+  }
   hipStream_t s = (hipStream_t)stream;
   return params->dtype == AFA_DTYPE_BF16 ? dispatch_d<DT_BF16>(a, s) : dispatch_d<DT_F16>(a, s);
 }
@@ -695,7 +828,7 @@ extern "C" int kernel_config_sparse_mla(int64_t cfg[5]) {
   if (!cfg) return AFA_E_NULL;
   cfg[0] = 13;  // external tensors
   cfg[1] = 0;   // runtime size parameters: all sizes travel in SparseMlaParams
-  cfg[2] = 0;   // no workspace
+  cfg[2] = 1;   // optional workspace: the per-token row-list plan
   cfg[3] = 256; // MI355X compute units
   cfg[4] = 4;   // SIMDs per compute unit
   return AFA_OK;
@@ -703,8 +836,9 @@ extern "C" int kernel_config_sparse_mla(int64_t cfg[5]) {
 
 extern "C" int workspace_size_sparse_mla(uint64_t* bytes, const SparseMlaParams* params) {
   if (!bytes) return -1;
-  (void)params;
-  *bytes = 0;
+  const int status = check_sparse(params);
+  if (status) return status;
+  *bytes = plan_bytes(params);
   return AFA_OK;
 }
 
@@ -729,5 +863,5 @@ extern "C" const char* kernel_metadata_sparse_mla(void) {
          "{\"name\":\"sinks\",\"dtype\":\"f32\",\"shape\":[\"H\"],\"access\":\"read\"},"
          "{\"name\":\"attention_out\",\"dtype\":\"DTYPE\",\"shape\":[\"T\",\"H\",\"D\"],"
          "\"access\":\"write\"}],"
-         "\"parameters\":\"SparseMlaParams\",\"disjoint_external\":true,\"workspace\":false}";
+         "\"parameters\":\"SparseMlaParams\",\"disjoint_external\":true,\"workspace\":true}";
 }

@@ -157,10 +157,15 @@ def sparse_mla(
         check_tensor("debug_rows", debug_rows, (T, S, 2), torch.int32, device)
     params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows)
     lib = _native.library()
+    # The workspace holds the per-token row-list plan (see workspace_size_sparse_mla);
+    # the caching allocator hands it out in stream order, so no host sync.
+    nbytes = ct.c_uint64(0)
+    _native.check(lib.workspace_size_sparse_mla(ct.byref(nbytes), ct.byref(params)), "workspace_size_sparse_mla")
+    workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=device) if nbytes.value else None
     status = lib.launch_sparse_mla(
         stream_handle(device),
         *(tensors[name].data_ptr() for name in tensors),
-        None,
+        None if workspace is None else workspace.data_ptr(),
         ct.byref(params),
     )
     _native.check(status, "launch_sparse_mla")

@@ -64,7 +64,11 @@ typedef struct SparseMlaParams {
  *   cmp_block_table i32 [B,MAX_SEQ/PAGE], cu_seqlens_q i32 [B+1],
  *   seqused_ori_kv i32 [B], seqused_cmp_kv i32 [B], cmp_residual_kv i32 [B],
  *   ori_topk_length i32 [T,1], sinks f32 [H], attention_out [T,H,D] (written).
- * `workspace` may be NULL: the fused kernel needs none (workspace_size = 0). */
+ * `workspace`: NULL, or at least workspace_size_sparse_mla() bytes of device
+ * memory that the call may overwrite. With a workspace a plan kernel first
+ * writes every token's selected-row list into it and the attention kernel
+ * reads the lists back; without one (or with params->debug_rows set) the
+ * attention kernel resolves the rows itself. Results are identical. */
 int launch_sparse_mla(void* stream, const void* q, const void* ori_kv, const void* cmp_kv,
                       const int32_t* cmp_sparse_indices, const int32_t* ori_block_table,
                       const int32_t* cmp_block_table, const int32_t* cu_seqlens_q,
@@ -118,8 +122,10 @@ const char* kernel_metadata_sparse_mla(void);
 const char* kernel_metadata_attention_target(void);
 const char* kernel_metadata_simple_attention(void);
 
-/* workspace_size_<k>: bytes of the optional workspace (0 for all three fused
- * kernels); returns -1 on a NULL output pointer (src/backend/workspace.py:100-130). */
+/* workspace_size_<k>: bytes of the optional workspace (sparse_mla: the row-list
+ * plan, T * 4 rounded up to 256 plus T * round_up(WINDOW + TOPK, 256) * 4;
+ * 0 for the two dense kernels); returns -1 on a NULL pointer and the
+ * launcher's status for invalid sparse parameters (src/backend/workspace.py:100-130). */
 int workspace_size_sparse_mla(uint64_t* bytes, const SparseMlaParams* params);
 int workspace_size_attention_target(uint64_t* bytes, int64_t Sq, int64_t Sk,
                                     const FaParams* params);

@@ -36,13 +36,23 @@ def test_kernel_config_and_workspace_queries(lib):
     for kernel, tensors in (("sparse_mla", 13), ("attention_target", 4), ("simple_attention", 4)):
         cfg = (ct.c_int64 * 5)()
         assert getattr(lib, f"kernel_config_{kernel}")(cfg) == 0
-        assert cfg[0] == tensors and cfg[2] == 0 and cfg[3] == 256 and cfg[4] == 4
+        has_workspace = kernel == "sparse_mla"
+        assert cfg[0] == tensors and cfg[2] == int(has_workspace) and cfg[3] == 256 and cfg[4] == 4
         meta = json.loads(getattr(lib, f"kernel_metadata_{kernel}")().decode())
         assert meta["kernel"] == kernel and len(meta["tensors"]) == tensors
-        assert meta["disjoint_external"] is True
+        assert meta["disjoint_external"] is True and meta["workspace"] is has_workspace
     size = ct.c_uint64(123)
-    assert lib.workspace_size_sparse_mla(ct.byref(size), None) == 0 and size.value == 0
+    # The sparse workspace is the row-list plan: T counts rounded up to 256
+    # bytes, then T lists of WINDOW + TOPK entries rounded up to 256.
+    params = good_params()
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
+    assert size.value == 256 + 16 * 768 * 4
+    params = good_params(T=100, TOPK=1000, S=1128)
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
+    assert size.value == 512 + 100 * 1280 * 4
+    assert lib.workspace_size_sparse_mla(ct.byref(size), None) == -1
     assert lib.workspace_size_sparse_mla(None, None) == -1
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(good_params(D=64))) == -2
     assert lib.workspace_size_attention_target(ct.byref(size), 8, 8, None) == 0 and size.value == 0
     assert lib.workspace_size_simple_attention(None, 64, 1) == -1
     assert b"gfx950" in lib.ascendflow_amd_version()
