@@ -252,9 +252,11 @@ __global__ __launch_bounds__(NTH) void sparse_plan_kernel(SparseArgs a) {
   const int token = blockIdx.x;
   Geometry geo;
   const int n = resolve_rows<NTH>(a, token, plan_list, wave_count, request_scratch, geo);
-  const int padded = (n + CHUNK - 1) / CHUNK * CHUNK;
+  // An empty list becomes one chunk of row 0 of ori_kv (every score masked),
+  // so every token has at least one chunk to stream.
+  const int padded = n > 0 ? (n + CHUNK - 1) / CHUNK * CHUNK : CHUNK;
   uint32_t* dst = a.plan_rows + (size_t)token * a.list_pad;
-  for (int r = threadIdx.x; r < padded; r += NTH) dst[r] = plan_list[r < n ? r : 0];
+  for (int r = threadIdx.x; r < padded; r += NTH) dst[r] = n > 0 ? plan_list[r < n ? r : 0] : 0u;
   if (threadIdx.x == 0) a.plan_count[token] = n;
 }
 
@@ -636,6 +638,373 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   }
 }
 
+// Persistent form for the plan workspace: one workgroup per CU walks the work
+// items worker, worker + G, ... (G workgroups; an item is one (token, BM-head
+// tile)) as ONE continuous chunk stream, so a token boundary costs no pipeline
+// drain and no dependent global round trip:
+//  - the KV ring, P slots and step parities run on across items;
+//  - only output waves fetch KV rows; each copies the row lists (and counts)
+//    of item j + 3 when item j starts, into a ring of four LDS lists;
+//  - score waves load Q and the sinks of item j + 1 into registers when item j
+//    starts and issue no other vector memory loads, so those loads have a
+//    whole item to land (vector loads of a wave complete in issue order, so a
+//    score-wave KV fetch would wait for them);
+//  - each item's running max starts at its sinks, its output accumulators are
+//    cleared on its first PV step, and 1/l travels through LDS slot item & 1.
+// The first item's Q goes through LDS as in sparse_mla_kernel.
+template <int DT, int D, int NQ, int NP>
+__global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(SparseArgs a) {
+  typedef typename B16<DT>::scalar scalar;
+  typedef typename B16<DT>::x8 x8;
+  typedef typename B16<DT>::x4 x4;
+  constexpr int NW = NQ + NP;
+  constexpr int BMH = 16 * NQ;
+  constexpr int UNITS = D / 8;
+  constexpr int ROW_BYTES = D * 2;
+  constexpr int QK_STEPS = D / 32;
+  constexpr int DPV = D / NP;
+  constexpr int PVT = DPV / 16;
+  constexpr int NO = NP * 64;                  // fetching threads (output waves)
+  constexpr int PIECES = CHUNK * UNITS / NO;   // 16-byte loads per output thread per chunk
+  constexpr int LISTS = 4;                     // row-list ring (items j .. j + 3)
+  static_assert(CHUNK * UNITS % NO == 0, "chunk must split evenly over the output waves");
+  static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
+  static_assert(DPV % 16 == 0 && (PVT <= 8 || (DPV / 8) % 16 == 0), "output feature range");
+
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NSTAGE][CHUNK * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][NQ][64];
+  __shared__ float alpha_lds[2][BMH];
+  __shared__ __attribute__((aligned(16))) int flag_lds[2][4];
+  __shared__ float linv_lds[2][BMH];
+  __shared__ __attribute__((aligned(16))) int count_lds[LISTS];
+  extern __shared__ __attribute__((aligned(16))) uint32_t lists[];  // [LISTS][list_pad]
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int g = lane >> 4, i16 = lane & 15;
+  const bool scorer = wave < NQ;
+  const int head_tiles = a.H / a.BM;
+  const int n_items = a.T * head_tiles;
+  const int G = (int)gridDim.x;
+  const int worker = (int)xcd_contiguous(blockIdx.x, gridDim.x);
+  const int J = (n_items - worker + G - 1) / G;  // items of this workgroup (>= 1)
+  auto item_token = [&](int j) { return (worker + j * G) / head_tiles; };
+  auto item_head0 = [&](int j) { return ((worker + j * G) % head_tiles) * a.BM; };
+  const uint32_t list_base = lds_address(lists);
+  auto list_address = [&](int j) { return list_base + (uint32_t)((j % LISTS) * a.list_pad) * 4u; };
+  // An item with no selected rows still runs one chunk (of row 0, all masked).
+  auto chunks_of = [&](int j) { return max(1, (count_lds[j % LISTS] + CHUNK - 1) / CHUNK); };
+
+  // Row list and count of item j: output waves split the 1 KiB units.
+  auto copy_list = [&](int j) {
+    const int token = item_token(j);
+    const uint32_t* src = a.plan_rows + (size_t)token * a.list_pad;
+    const uint32_t dst = list_address(j);
+    if (wave == NQ && lane == 0)
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+                       :: "s"(lds_address(&count_lds[j % LISTS])), "v"(0u), "s"(a.plan_count + token) : "memory");
+    for (int u = wave - NQ; u < a.list_pad / 256; u += NP)
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                       :: "s"(dst + (uint32_t)u * 1024u), "v"((uint32_t)lane * 16u), "s"(src + u * 256) : "memory");
+  };
+
+  // ---- prologue: lists of items 0..2, Q of item 0 through ring tiles 1-2 ----
+  const uint32_t q_lds = lds_address(kv_lds[1]);
+  constexpr int Q_LOADS = BMH * ROW_BYTES / 1024;
+  static_assert(BMH * ROW_BYTES <= 2 * CHUNK * ROW_BYTES, "Q tile must fit ring tiles 1 and 2");
+  static_assert(Q_LOADS % NW == 0, "Q tile must split evenly over the waves");
+  constexpr int Q_LOADS_PER_WAVE = Q_LOADS / NW;
+  if (!scorer)
+    for (int j = 0; j < J && j < LISTS - 1; ++j) copy_list(j);
+  {
+    const char* q_src = (const char*)a.q + ((size_t)item_token(0) * a.H + item_head0(0)) * ROW_BYTES;
+#pragma unroll
+    for (int k0 = 0; k0 < Q_LOADS; k0 += NW) {
+      const int k = k0 + wave;
+      const int pos = k * 64 + lane;
+      const int r = pos / UNITS, u = pos % UNITS;
+      const uint32_t off = (uint32_t)(r * ROW_BYTES + ((u ^ (r & 15)) << 4));
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                       :: "s"(q_lds + (uint32_t)k * 1024u), "v"(off), "s"(q_src) : "memory");
+    }
+  }
+  // Lists landed (Q may still be in flight).
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (Q_LOADS_PER_WAVE & 15) | ((Q_LOADS_PER_WAVE >> 4) << 14));
+  block_barrier();
+
+  // ---- KV fetch by the output waves ------------------------------------------
+  constexpr bool ROW_LOADS = (UNITS == 64);
+  const char* ori = (const char*)a.ori_kv;
+  const char* cmp = (const char*)a.cmp_kv;
+  const uint32_t kv_base = lds_address(kv_lds[0]);
+  auto tile_address = [&](int s) {
+    return opaque_uniform(kv_base + (uint32_t)(s % NSTAGE) * (CHUNK * ROW_BYTES));
+  };
+  const int ow = wave - NQ;  // output wave index (fetch role)
+  uint32_t unit_offset[PIECES];
+#pragma unroll
+  for (int p = 0; p < PIECES; ++p) unit_offset[p] = (uint32_t)((lane ^ ((ow * PIECES + p) & 15)) << 4);
+  // Entries of the next chunk to fetch (ROW_LOADS), read one step ahead.
+  uint32_t entry_next[PIECES];
+  auto read_entries = [&](int j, int c) {
+    const AFA_LDS uint32_t* l = lds_at<uint32_t>(list_address(j));
+#pragma unroll
+    for (int p = 0; p < PIECES; ++p) entry_next[p] = l[c * CHUNK + ow * PIECES + p];
+  };
+  // Chunk (j, c) of the stream into tile s % NSTAGE; then the entries of (nj_, nc_).
+  auto fetch = [&](int s, int j, int c, bool next_valid, int nj_, int nc_) {
+    const uint32_t tile = tile_address(s);
+    if constexpr (ROW_LOADS) {
+#pragma unroll
+      for (int p = 0; p < PIECES; ++p) {
+        const int r = ow * PIECES + p;
+        const uint32_t e = __builtin_amdgcn_readfirstlane(entry_next[p]);
+        const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES;
+        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                         :: "s"(tile + (uint32_t)(r * ROW_BYTES)), "v"(unit_offset[p]), "s"(row) : "memory");
+      }
+      if (next_valid) read_entries(nj_, nc_);
+    } else {
+      const AFA_LDS uint32_t* l = lds_at<uint32_t>(list_address(j));
+      const int otid = tid - NQ * 64;
+#pragma unroll
+      for (int p = 0; p < PIECES; ++p) {
+        const int flat = otid + p * NO;
+        const int r = flat / UNITS, upos = flat % UNITS;
+        const uint32_t e = l[c * CHUNK + r];
+        const char* src = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES + ((upos ^ (r & 15)) << 4);
+        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                         :: "s"(tile + (uint32_t)((ow * 64 + p * NO) * 16)), "v"(src) : "memory");
+      }
+    }
+  };
+
+  // ---- stream cursors (uniform and identical in every wave) ------------------
+  // Score cursor (j, c) of item j's chunk c with nj chunks; the fetch cursor is
+  // one chunk ahead of it.
+  int j = 0, c = 0, nj = chunks_of(0);
+  auto advance = [&](int& jj, int& cc, int& nn) -> bool {  // false at the end of the stream
+    if (++cc < nn) return true;
+    ++jj;
+    cc = 0;
+    if (jj >= J) return false;
+    nn = chunks_of(jj);
+    return true;
+  };
+  // First fetch: chunk (0, 0) into tile 0.
+  if (!scorer) {
+    if constexpr (ROW_LOADS) read_entries(0, 0);
+    int j1 = 0, c1 = 0, n1 = nj;
+    const bool v1 = advance(j1, c1, n1);
+    fetch(0, 0, 0, v1, j1, c1);
+    // Q has landed once at most the PIECES loads of the fetch are in flight.
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  }
+  block_barrier();
+
+  if (scorer) {
+    // ---- score waves ------------------------------------------------------------
+    const float scale_log2 = a.scale * LOG2E;
+    const int ra = sigma(i16);
+    uint32_t qk_base[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) qk_base[b] = (uint32_t)(ra * ROW_BYTES + (((4 * b + g) ^ (ra & 15)) << 4));
+    x8 qf[QK_STEPS], qf_next[QK_STEPS];
+    {
+      const int r = 16 * wave + i16;
+#pragma unroll
+      for (int k = 0; k < QK_STEPS; ++k)
+        qf[k] = *lds_at<x8>(q_lds + (uint32_t)(r * ROW_BYTES + (((4 * k + g) ^ (r & 15)) << 4)));
+    }
+    float sink = a.sinks[item_head0(0) + 16 * wave + i16] * LOG2E, sink_next = 0.f;
+    float m_run = 0.f, l_run = 0.f;
+    for (int s = 0;; ++s) {
+      if (j >= J) {  // stream done: one more barrier for the last PV, then leave
+        block_barrier();
+        break;
+      }
+      block_barrier();
+      if (c == 0) {
+        if (j > 0) {
+#pragma unroll
+          for (int k = 0; k < QK_STEPS; ++k) qf[k] = qf_next[k];
+          sink = sink_next;
+        }
+        m_run = sink;
+        l_run = g == 0 ? 1.0f : 0.0f;  // e^(sink - m) counted once per head
+        if (j + 1 < J) {
+          const int head = item_head0(j + 1) + 16 * wave + i16;
+          const scalar* q_row = (const scalar*)a.q + ((size_t)item_token(j + 1) * a.H + head) * D + 8 * g;
+#pragma unroll
+          for (int k = 0; k < QK_STEPS; ++k) qf_next[k] = *(const x8*)(q_row + 32 * k);
+          sink_next = a.sinks[head] * LOG2E;
+        }
+      }
+      // S^T of this chunk: fragment reads LOOK_QK k-steps ahead of the MFMAs.
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      {
+        const uint32_t tile = tile_address(s);
+        uint32_t base[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) base[b] = opaque(tile + qk_base[b]);
+        x8 ka0[QK_STEPS], ka1[QK_STEPS];
+        auto load = [&](int k) {
+          const AFA_LDS uint8_t* q = lds_at<uint8_t>(base[k & 3]) + (k >> 2) * 256;
+          ka0[k] = *(const AFA_LDS x8*)q;
+          ka1[k] = *(const AFA_LDS x8*)(q + 16 * ROW_BYTES);
+        };
+#pragma unroll
+        for (int k = 0; k < LOOK_QK && k < QK_STEPS; ++k) load(k);
+#pragma unroll
+        for (int k = 0; k < QK_STEPS; ++k) {
+          if (k + LOOK_QK < QK_STEPS) load(k + LOOK_QK);
+          s0 = B16<DT>::mfma(ka0[k], qf[k], s0);
+          s1 = B16<DT>::mfma(ka1[k], qf[k], s1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      const int slot = s & 1;
+      float x0[4], x1[4];
+      float cmax = -INFINITY;
+      const int live = count_lds[j % LISTS] - c * CHUNK;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x0[k] = s0[k];
+        x1[k] = s1[k];
+        if (live < CHUNK) {
+          const int row = sigma(4 * g + k);
+          x0[k] = (row < live) ? x0[k] : -INFINITY;
+          x1[k] = (16 + row < live) ? x1[k] : -INFINITY;
+        }
+        cmax = fmaxf(cmax, fmaxf(x0[k], x1[k]));
+      }
+      cmax = max_over_lane_groups(cmax);
+      const float m_new = fmaxf(m_run, cmax * scale_log2);
+      const bool raise = __ballot(m_new > m_run + TAU) != 0ull;
+      if (raise) {
+        const float alpha = fast_exp2(m_run - m_new);
+        l_run *= alpha;
+        m_run = m_new;
+        if (g == 0) alpha_lds[slot][16 * wave + i16] = alpha;
+      }
+      if (lane == 0) flag_lds[slot][wave] = raise ? 1 : 0;
+      const float neg_m = -m_run;
+      float psum = 0.f;
+      x8 p8;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float p0 = fast_exp2(__builtin_fmaf(x0[k], scale_log2, neg_m));
+        const float p1 = fast_exp2(__builtin_fmaf(x1[k], scale_log2, neg_m));
+        psum += p0 + p1;
+        p8[k] = (scalar)p0;
+        p8[4 + k] = (scalar)p1;
+      }
+      l_run += psum;
+      p_lds[slot][wave][lane] = __builtin_bit_cast(u32x4, p8);
+      if (c == nj - 1) {
+        const float l = sum_over_lane_groups(l_run);
+        if (g == 0) linv_lds[j & 1][16 * wave + i16] = 1.0f / l;
+      }
+      advance(j, c, nj);
+    }
+  } else {
+    // ---- output waves: fetch, then O^T[features, heads] += V^T * P^T ----------
+    const int dbase = ow * DPV;
+    f32x4 o[NQ][PVT];
+    constexpr int NB = PVT < 8 ? PVT : 8;
+    const int rt = sigma(4 * g + (i16 >> 2));
+    uint32_t tr_base[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      tr_base[b] = (uint32_t)(rt * ROW_BYTES + (((dbase / 8 + 2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
+    int oj = -1, oc = 0, onj = 0;  // output cursor: the score cursor of the previous step
+    for (int s = 0;; ++s) {
+      const bool score_active = j < J;
+      if (!score_active && oj < 0) break;
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      block_barrier();
+      if (score_active) {
+        // Fetch the chunk after (j, c), and read the entries of the one after that.
+        int j1 = j, c1 = c, n1 = nj;
+        if (advance(j1, c1, n1)) {
+          int j2 = j1, c2 = c1, n2 = n1;
+          const bool v2 = advance(j2, c2, n2);
+          fetch(s + 1, j1, c1, v2, j2, c2);
+        }
+        if (c == 0 && j + LISTS - 1 < J) copy_list(j + LISTS - 1);
+      }
+      if (oj >= 0) {
+        const int slot = (s - 1) & 1;
+        if (oc == 0) {
+#pragma unroll
+          for (int ht = 0; ht < NQ; ++ht)
+#pragma unroll
+            for (int t = 0; t < PVT; ++t) o[ht][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        const u32x4 flags = *lds_at<u32x4>(lds_address(flag_lds[slot]));
+        x8 pb[NQ];
+#pragma unroll
+        for (int ht = 0; ht < NQ; ++ht) pb[ht] = __builtin_bit_cast(x8, p_lds[slot][ht][lane]);
+        const uint32_t tile = tile_address(s - 1);
+        uint32_t vbase[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) vbase[b] = opaque(tile + tr_base[b]);
+        x4 vlo[PVT], vhi[PVT];
+        auto load_step = [&](int t) {
+          const AFA_LDS uint8_t* p = lds_at<uint8_t>(vbase[t % NB]) + (t / NB) * 256;
+          vlo[t] = B16<DT>::read_tr((const AFA_LDS void*)p);
+          vhi[t] = B16<DT>::read_tr((const AFA_LDS void*)(p + 16 * ROW_BYTES));
+        };
+#pragma unroll
+        for (int t = 0; t < LOOK && t < PVT; ++t) load_step(t);
+#pragma unroll
+        for (int ht = 0; ht < NQ; ++ht) {
+          if (__builtin_amdgcn_readfirstlane(flags[ht])) {
+            const float alpha = alpha_lds[slot][16 * ht + i16];
+#pragma unroll
+            for (int t = 0; t < PVT; ++t) o[ht][t] *= alpha;
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < PVT; ++t) {
+          if (t + LOOK < PVT) load_step(t + LOOK);
+          const x8 v = {vlo[t][0], vlo[t][1], vlo[t][2], vlo[t][3], vhi[t][0], vhi[t][1], vhi[t][2], vhi[t][3]};
+#pragma unroll
+          for (int ht = 0; ht < NQ; ++ht) o[ht][t] = B16<DT>::mfma(v, pb[ht], o[ht][t]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (oc == onj - 1) {
+          // Normalise and store item oj: this lane holds head head0 + 16ht +
+          // i16, features dbase + 16t + 4g + i.
+          const int token = item_token(oj), head0 = item_head0(oj);
+#pragma unroll
+          for (int ht = 0; ht < NQ; ++ht) {
+            const float inv = linv_lds[oj & 1][16 * ht + i16];
+            scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + 16 * ht + i16) * D + dbase + 4 * g;
+#pragma unroll
+            for (int t = 0; t < PVT; ++t) {
+              x4 v;
+#pragma unroll
+              for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
+              *(x4*)(out_row + 16 * t) = v;
+            }
+          }
+        }
+      }
+      if (score_active) {
+        oj = j;
+        oc = c;
+        onj = nj;
+        advance(j, c, nj);
+      } else {
+        oj = -1;
+      }
+    }
+  }
+}
+
 // Gather image: one block per token, slot-major copy of the selected rows
 // through the fused kernel's slot resolution (resolve_slot, row_pointer).
 template <int DT>
@@ -739,17 +1108,47 @@ static int fits_lds(K kernel, size_t dynamic_bytes) {
   return attr.sharedSizeBytes + dynamic_bytes <= LDS_BYTES ? AFA_OK : AFA_E_SHAPE;
 }
 
+// Compute units of the current device (one persistent workgroup each).
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  return cus;
+}
+
 template <int DT, int D, int NQ, int NP>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
-  const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
-  if (fit) return fit;
   if (a.plan_rows != nullptr) {
+    // Plan kernel, then the persistent kernel over the plan (four row lists)
+    // when every CU gets at least two items (it removes the per-item start,
+    // which costs more than its own overheads only then) and four lists fit
+    // next to its ring; otherwise the one-item-per-workgroup kernel.
+    const size_t lists = 4 * lds;
+    static int cus = 0;
+    if (cus == 0) cus = device_cus();
+    const int64_t items = (int64_t)a.T * (a.H / a.BM);
+    const bool persistent = items >= 2 * (int64_t)cus &&
+                            fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP>, lists) == AFA_OK;
+    if (!persistent) {
+      const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
+      if (fit) return fit;
+    }
     constexpr int PLAN_THREADS = 256;
     hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
-    const hipError_t e = hipGetLastError();
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
+    if (!persistent) {
+      const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
+      hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
+      return (int)hipGetLastError();
+    }
+    const unsigned grid = (unsigned)cus;
+    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP>), dim3(grid), dim3((NQ + NP) * 64), lists, stream, a);
+    return (int)hipGetLastError();
   }
+  const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
+  if (fit) return fit;
   const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
   hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   return (int)hipGetLastError();

@@ -63,6 +63,44 @@ def test_validation_cases_match_oracle(device, case, variant):
     assert_close(actual, sr.oracle_fp32(data, policy), policy["DTYPE"])
     if case == "empty":
         assert np.all(actual == 0)
+    # Without the debug image the call takes the plan workspace path (plan
+    # kernel + attention over the plan); it must give the same bits.
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    fused = tensors["attention_out"].clone()
+    tensors["attention_out"].fill_(float("nan"))
+    sparse_mla(*call_args(tensors), **call_kwargs(policy))
+    torch.cuda.synchronize()
+    assert torch.equal(fused, tensors["attention_out"]), "plan path differs from the in-kernel row resolution"
+    assert guard_intact(tensors), "kernel wrote past attention_out"
+
+
+@pytest.mark.parametrize("variant", [v for v in VARIANTS if "topk" not in v])
+def test_persistent_stream_matches_fused_and_oracle(device, variant):
+    """T = 544 tokens: at least two work items per CU, so the plan path runs
+    the persistent kernel, whose workgroups stream many tokens (and, with
+    BM = 32, both head tiles of a token) through one pipeline. Its output must
+    equal the in-kernel row resolution bit for bit, and the oracle on a sample
+    that includes empty and one-row selections."""
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    policy = sr.default_policy(B=6, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
+    data = sr.inputs(policy, "mixed")
+    tensors = to_device(data, policy, device)
+    debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug)
+    torch.cuda.synchronize()
+    fused = tensors["attention_out"].clone()
+    tensors["attention_out"].fill_(float("nan"))
+    sparse_mla(*call_args(tensors), **call_kwargs(policy))
+    torch.cuda.synchronize()
+    assert guard_intact(tensors), "kernel wrote past attention_out"
+    assert torch.equal(fused, tensors["attention_out"]), "persistent stream differs from the in-kernel row resolution"
+    rows = (debug[..., 0] >= 0).sum(dim=1).cpu().numpy()
+    rng = np.random.default_rng(11)
+    tokens = sorted({0, 1, 543, *np.flatnonzero(rows <= 1)[:8].tolist(), *rng.choice(544, 24, replace=False).tolist()})
+    actual = tensors["attention_out"][torch.as_tensor(tokens, device=device)].float().cpu().numpy()
+    assert_close(actual, sr.oracle_fp32(data, policy, tokens), policy["DTYPE"])
 
 
 def test_relaunch_is_bitwise_deterministic(device):
