@@ -10,10 +10,11 @@
 //   1. resolve the token's request and window/compressed bounds
 //      (gather.py:8-35, attention.py:339-341) and compact every selected row
 //      (window positions, then compressed ranks, duplicates kept) into an LDS
-//      row list of physical row ids. With a workspace, a plan kernel does this
-//      for every token first (three dependent global round trips that would
-//      otherwise leave the CU's matrix cores idle at each token start) and the
-//      main kernel copies the token's list into LDS with one load-to-LDS pass;
+//      row list of physical row ids. With a workspace and at least two work
+//      items per CU, a plan kernel does this for every token first and a
+//      persistent form (sparse_mla_persistent_kernel) streams the tokens of
+//      each CU through one pipeline, so the three dependent global round trips
+//      and the pipeline fill no longer idle the matrix cores at token starts;
 //   2. stream the listed rows through a 3-stage ring of XOR-swizzled LDS
 //      tiles of CHUNK rows with the load-to-LDS path (global_load_lds_dwordx4,
 //      one wave load per 1 KiB row when D = 512);
@@ -324,8 +325,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   const int token = (int)(logical / head_tiles);
   const int head0 = (int)(logical % head_tiles) * a.BM;
 
-  // ---- 1-2. the token's row list in LDS (from the plan, or resolved here)
-  // and Q. Q (BMH contiguous rows of D features) is copied with the
+  // ---- 1-2. the token's row list in LDS and Q. Q (BMH contiguous rows of D features) is copied with the
   // load-to-LDS path in coalesced 1 KiB wave loads into ring tiles 1 and 2,
   // which stay unused until the first pipeline step, with the KV rows' unit
   // swizzle; each score wave then reads its B-operand fragments (S^T = KV *
@@ -352,28 +352,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   constexpr int Q_LOADS_PER_WAVE = (Q_LOADS + NW - 1) / NW;
   __shared__ int request_scratch[NW];
   int n_rows;
-  if (a.plan_rows != nullptr) {
-    // Output waves copy the count and the padded list (whole KiB units) first;
-    // every wave then copies its share of Q. The list is waited for with the
-    // Q loads still in flight.
-    if (!scorer) {
-      const uint32_t* src = a.plan_rows + (size_t)token * a.list_pad;
-      const uint32_t list_base = lds_address(row_list);
-      if (wave == NQ && lane == 0)
-        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
-                         :: "s"(lds_address(request_scratch)), "v"(0u), "s"(a.plan_count + token) : "memory");
-      for (int u = wave - NQ; u < a.list_pad / 256; u += NP) {
-        const uint32_t dst = list_base + (uint32_t)u * 1024u;
-        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                         :: "s"(dst), "v"((uint32_t)lane * 16u), "s"(src + u * 256) : "memory");
-      }
-    }
-    copy_q();
-    if (!scorer)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (Q_LOADS_PER_WAVE & 15) | ((Q_LOADS_PER_WAVE >> 4) << 14));
-    block_barrier();
-    n_rows = request_scratch[0];
-  } else {
+  {
     Geometry geo;
     n_rows = resolve_rows<NT>(a, token, row_list, wave_count, request_scratch, geo);
     // Pad the last chunk with a real row so every load is unconditional; the
@@ -1122,30 +1101,22 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   if (a.plan_rows != nullptr) {
     // Plan kernel, then the persistent kernel over the plan (four row lists)
     // when every CU gets at least two items (it removes the per-item start,
-    // which costs more than its own overheads only then) and four lists fit
-    // next to its ring; otherwise the one-item-per-workgroup kernel.
-    const size_t lists = 4 * lds;
+    // which outweighs a second kernel only then) and four lists fit next to
+    // its ring. Otherwise the one-item-per-workgroup kernel resolves its rows.
     static int cus = 0;
     if (cus == 0) cus = device_cus();
     const int64_t items = (int64_t)a.T * (a.H / a.BM);
-    const bool persistent = items >= 2 * (int64_t)cus &&
-                            fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP>, lists) == AFA_OK;
-    if (!persistent) {
-      const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
-      if (fit) return fit;
-    }
-    constexpr int PLAN_THREADS = 256;
-    hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-    if (!persistent) {
-      const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
-      hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
+    const size_t lists = 4 * lds;
+    if (items >= 2 * (int64_t)cus &&
+        fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP>, lists) == AFA_OK) {
+      constexpr int PLAN_THREADS = 256;
+      hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return (int)e;
+      hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP>), dim3((unsigned)cus),
+                         dim3((NQ + NP) * 64), lists, stream, a);
       return (int)hipGetLastError();
     }
-    const unsigned grid = (unsigned)cus;
-    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP>), dim3(grid), dim3((NQ + NP) * 64), lists, stream, a);
-    return (int)hipGetLastError();
   }
   const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
   if (fit) return fit;

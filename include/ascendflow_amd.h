@@ -65,10 +65,12 @@ typedef struct SparseMlaParams {
  *   seqused_ori_kv i32 [B], seqused_cmp_kv i32 [B], cmp_residual_kv i32 [B],
  *   ori_topk_length i32 [T,1], sinks f32 [H], attention_out [T,H,D] (written).
  * `workspace`: NULL, or at least workspace_size_sparse_mla() bytes of device
- * memory that the call may overwrite. With a workspace a plan kernel first
- * writes every token's selected-row list into it and the attention kernel
- * reads the lists back; without one (or with params->debug_rows set) the
- * attention kernel resolves the rows itself. Results are identical. */
+ * memory that the call may overwrite. With a workspace and at least two work
+ * items (token x BM-head tile) per compute unit, a plan kernel first writes
+ * every token's selected-row list into it and a persistent attention kernel
+ * streams the tokens of each compute unit over those lists; otherwise (or with
+ * params->debug_rows set) one workgroup per item resolves its rows itself.
+ * Results are bit-identical either way. */
 int launch_sparse_mla(void* stream, const void* q, const void* ori_kv, const void* cmp_kv,
                       const int32_t* cmp_sparse_indices, const int32_t* ori_block_table,
                       const int32_t* cmp_block_table, const int32_t* cu_seqlens_q,
