@@ -58,7 +58,7 @@ class SparseMlaParams(ct.Structure):
         ("BM", ct.c_int32),
         ("dtype", ct.c_int32),
         ("scale", ct.c_float),
-        ("reserved", ct.c_int32),
+        ("parts", ct.c_int32),
         ("debug_rows", ct.c_void_p),
     ]
 

@@ -30,6 +30,7 @@
 //
 // K and V are the same gathered rows; each row is read from global memory
 // once per workgroup and from LDS once per score wave and once per output wave.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -38,6 +39,7 @@
 namespace afa {
 
 constexpr int CHUNK = 32;                 // rows per LDS stage
+constexpr int MAX_PARTS = 8;              // most parts a token's chunk list is split into
 constexpr uint32_t CMP_BIT = 0x80000000u; // row-list tag: row lives in cmp_kv
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -58,8 +60,11 @@ struct SparseArgs {
   int32_t* debug_rows;
   uint32_t* plan_rows;   // workspace: [T][list_pad] padded row lists, or null
   int32_t* plan_count;   // workspace: [T] selected rows per token
+  float* partials;       // workspace: [split tiles][parts][output waves][record] of split work items
   int32_t B, T, H, D, PAGE, RATIO, table_width, ori_blocks, cmp_blocks, WINDOW, TOPK, S, BM;
   int32_t list_pad;      // row-list capacity: WINDOW + TOPK rounded up to 256 (whole KiB)
+  int32_t parts;         // parts each split (token, head tile) is divided into (persistent kernel)
+  int32_t split_from;    // first split (token, head tile) key; keys below it run whole
   float scale;
 };
 
@@ -617,21 +622,50 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   }
 }
 
-// Persistent form for the plan workspace: one workgroup per CU walks the work
-// items worker, worker + G, ... (G workgroups; an item is one (token, BM-head
-// tile)) as ONE continuous chunk stream, so a token boundary costs no pipeline
-// drain and no dependent global round trip:
-//  - the KV ring, P slots and step parities run on across items;
-//  - only output waves fetch KV rows; each copies the row lists (and counts)
-//    of item j + 3 when item j starts, into a ring of four LDS lists;
+// A token's chunk list split into P parts: part p covers list chunks
+// [p * n / P, (p + 1) * n / P) of the token's n = max(1, ceil(count / CHUNK))
+// chunks. An empty part (n < P) streams one fully masked chunk (list chunk 0),
+// so every work item has at least one chunk and one partial result.
+struct PartRange {
+  int first;  // first list chunk of the part
+  int n;      // list chunks of the part; 0 for the masked placeholder
+};
+__device__ __forceinline__ PartRange part_range(int count, int part, int parts) {
+  const int nch = max(1, (count + CHUNK - 1) / CHUNK);
+  const int c0 = part * nch / parts, c1 = (part + 1) * nch / parts;
+  return PartRange{c0, c1 - c0};
+}
+
+// Stream position: chunk c of work item j (workgroup-local index), whose part
+// starts at list chunk `first` and holds n list chunks (0: one masked chunk).
+struct Cursor {
+  int j, c, first, n;
+  __device__ __forceinline__ int chunks() const { return n > 0 ? n : 1; }
+  __device__ __forceinline__ int list_chunk() const { return n > 0 ? first + c : 0; }
+};
+
+// Persistent form for the plan workspace: one workgroup per CU walks its work
+// items worker, worker + G, ... (G workgroups) as ONE continuous chunk stream,
+// so an item boundary costs no pipeline drain and no dependent global round
+// trip. Work items are the (token, BM-head tile) keys below split_from, whole,
+// then P parts of each key from split_from on: a split key's chunk list is
+// divided over P workgroups (so the last round of a short stream, such as
+// decode, keeps every CU busy to the end) and each part stores its
+// unnormalised (m, l, O) record for sparse_merge_kernel, which runs next.
+//  - the KV ring of NS tiles, P slots and step parities run on across items;
+//    output waves fetch KV rows AHEAD = NS - 2 chunks ahead of the score waves
+//    (two chunks in flight hide the HBM latency of short streams);
+//  - output waves copy the row list (and count) of item j + LISTS - 1 when
+//    item j starts, into a ring of LISTS LDS lists;
 //  - score waves load Q and the sinks of item j + 1 into registers when item j
 //    starts and issue no other vector memory loads, so those loads have a
 //    whole item to land (vector loads of a wave complete in issue order, so a
 //    score-wave KV fetch would wait for them);
-//  - each item's running max starts at its sinks, its output accumulators are
-//    cleared on its first PV step, and 1/l travels through LDS slot item & 1.
+//  - each item's running max starts at its sinks (part 0 alone counts the
+//    sink's e^(sink - m)), its output accumulators are cleared on its first PV
+//    step, and its running max and denominator travel through LDS slot item & 1.
 // The first item's Q goes through LDS as in sparse_mla_kernel.
-template <int DT, int D, int NQ, int NP>
+template <int DT, int D, int NQ, int NP, int NS>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
@@ -645,16 +679,20 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   constexpr int PVT = DPV / 16;
   constexpr int NO = NP * 64;                  // fetching threads (output waves)
   constexpr int PIECES = CHUNK * UNITS / NO;   // 16-byte loads per output thread per chunk
-  constexpr int LISTS = 4;                     // row-list ring (items j .. j + 3)
+  constexpr int AHEAD = NS - 2;                // chunks fetched ahead of the score waves
+  constexpr int LISTS = AHEAD + 3;             // row-list ring (items j - 1 .. j + AHEAD + 1 in use)
+  constexpr int REC = BMH * DPV + 2 * BMH;     // floats of one output wave's partial record
+  static_assert(NS == 3 || NS == 4, "KV ring of 3 or 4 tiles");
   static_assert(CHUNK * UNITS % NO == 0, "chunk must split evenly over the output waves");
   static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
   static_assert(DPV % 16 == 0 && (PVT <= 8 || (DPV / 8) % 16 == 0), "output feature range");
+  static_assert(NQ == NP && NQ <= 4, "one score and one output wave per SIMD");
 
-  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NSTAGE][CHUNK * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NS][CHUNK * ROW_BYTES];
   __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][NQ][64];
   __shared__ float alpha_lds[2][BMH];
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];
-  __shared__ float linv_lds[2][BMH];
+  __shared__ float ml_lds[2][2][BMH];  // item parity: running max (log2 units), denominator
   __shared__ __attribute__((aligned(16))) int count_lds[LISTS];
   extern __shared__ __attribute__((aligned(16))) uint32_t lists[];  // [LISTS][list_pad]
 
@@ -663,16 +701,41 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   const int g = lane >> 4, i16 = lane & 15;
   const bool scorer = wave < NQ;
   const int head_tiles = a.H / a.BM;
-  const int n_items = a.T * head_tiles;
+  const int P = a.parts, S0 = a.split_from;
+  const int n_items = S0 + (a.T * head_tiles - S0) * P;
   const int G = (int)gridDim.x;
   const int worker = (int)xcd_contiguous(blockIdx.x, gridDim.x);
-  const int J = (n_items - worker + G - 1) / G;  // items of this workgroup (>= 1)
-  auto item_token = [&](int j) { return (worker + j * G) / head_tiles; };
-  auto item_head0 = [&](int j) { return ((worker + j * G) % head_tiles) * a.BM; };
+  const int J = (n_items - worker + G - 1) / G;  // items of this workgroup (>= 1: G <= n_items)
+  // Item i < S0 is key i, whole; item S0 + k * P + p is part p of key S0 + k.
+  auto item_key = [&](int j) {
+    const int i = worker + j * G;
+    return i < S0 ? i : S0 + (i - S0) / P;
+  };
+  auto item_part = [&](int j) {
+    const int i = worker + j * G;
+    return i < S0 ? 0 : (i - S0) % P;
+  };
+  auto item_parts = [&](int j) { return worker + j * G < S0 ? 1 : P; };
+  auto item_token = [&](int j) { return item_key(j) / head_tiles; };
+  auto item_head0 = [&](int j) { return (item_key(j) % head_tiles) * a.BM; };
   const uint32_t list_base = lds_address(lists);
   auto list_address = [&](int j) { return list_base + (uint32_t)((j % LISTS) * a.list_pad) * 4u; };
-  // An item with no selected rows still runs one chunk (of row 0, all masked).
-  auto chunks_of = [&](int j) { return max(1, (count_lds[j % LISTS] + CHUNK - 1) / CHUNK); };
+  auto start = [&](Cursor& k, int j) {
+    const PartRange r = part_range(count_lds[j % LISTS], item_part(j), item_parts(j));
+    k.j = j;
+    k.c = 0;
+    k.first = r.first;
+    k.n = r.n;
+  };
+  auto advance = [&](Cursor& k) -> bool {  // false at the end of the stream (k.j becomes J)
+    if (++k.c < k.chunks()) return true;
+    if (k.j + 1 >= J) {
+      k.j = J;
+      return false;
+    }
+    start(k, k.j + 1);
+    return true;
+  };
 
   // Row list and count of item j: output waves split the 1 KiB units.
   auto copy_list = [&](int j) {
@@ -687,10 +750,10 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
                        :: "s"(dst + (uint32_t)u * 1024u), "v"((uint32_t)lane * 16u), "s"(src + u * 256) : "memory");
   };
 
-  // ---- prologue: lists of items 0..2, Q of item 0 through ring tiles 1-2 ----
-  const uint32_t q_lds = lds_address(kv_lds[1]);
+  // ---- prologue: lists of items 0..LISTS-2, Q of item 0 through the last two ring tiles ----
+  const uint32_t q_lds = lds_address(kv_lds[NS - 2]);
   constexpr int Q_LOADS = BMH * ROW_BYTES / 1024;
-  static_assert(BMH * ROW_BYTES <= 2 * CHUNK * ROW_BYTES, "Q tile must fit ring tiles 1 and 2");
+  static_assert(BMH * ROW_BYTES <= 2 * CHUNK * ROW_BYTES, "Q tile must fit two ring tiles");
   static_assert(Q_LOADS % NW == 0, "Q tile must split evenly over the waves");
   constexpr int Q_LOADS_PER_WAVE = Q_LOADS / NW;
   if (!scorer)
@@ -717,21 +780,21 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   const char* cmp = (const char*)a.cmp_kv;
   const uint32_t kv_base = lds_address(kv_lds[0]);
   auto tile_address = [&](int s) {
-    return opaque_uniform(kv_base + (uint32_t)(s % NSTAGE) * (CHUNK * ROW_BYTES));
+    return opaque_uniform(kv_base + (uint32_t)(s % NS) * (CHUNK * ROW_BYTES));
   };
   const int ow = wave - NQ;  // output wave index (fetch role)
   uint32_t unit_offset[PIECES];
 #pragma unroll
   for (int p = 0; p < PIECES; ++p) unit_offset[p] = (uint32_t)((lane ^ ((ow * PIECES + p) & 15)) << 4);
-  // Entries of the next chunk to fetch (ROW_LOADS), read one step ahead.
+  // Entries of the next chunk to fetch (ROW_LOADS), read one fetch ahead.
   uint32_t entry_next[PIECES];
-  auto read_entries = [&](int j, int c) {
-    const AFA_LDS uint32_t* l = lds_at<uint32_t>(list_address(j));
+  auto read_entries = [&](const Cursor& k) {
+    const AFA_LDS uint32_t* l = lds_at<uint32_t>(list_address(k.j));
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) entry_next[p] = l[c * CHUNK + ow * PIECES + p];
+    for (int p = 0; p < PIECES; ++p) entry_next[p] = l[k.list_chunk() * CHUNK + ow * PIECES + p];
   };
-  // Chunk (j, c) of the stream into tile s % NSTAGE; then the entries of (nj_, nc_).
-  auto fetch = [&](int s, int j, int c, bool next_valid, int nj_, int nc_) {
+  // The chunk at cursor k into ring tile s % NS (ROW_LOADS: entries already read).
+  auto fetch = [&](int s, const Cursor& k) {
     const uint32_t tile = tile_address(s);
     if constexpr (ROW_LOADS) {
 #pragma unroll
@@ -742,15 +805,14 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
         __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                          :: "s"(tile + (uint32_t)(r * ROW_BYTES)), "v"(unit_offset[p]), "s"(row) : "memory");
       }
-      if (next_valid) read_entries(nj_, nc_);
     } else {
-      const AFA_LDS uint32_t* l = lds_at<uint32_t>(list_address(j));
+      const AFA_LDS uint32_t* l = lds_at<uint32_t>(list_address(k.j));
       const int otid = tid - NQ * 64;
 #pragma unroll
       for (int p = 0; p < PIECES; ++p) {
         const int flat = otid + p * NO;
         const int r = flat / UNITS, upos = flat % UNITS;
-        const uint32_t e = l[c * CHUNK + r];
+        const uint32_t e = l[k.list_chunk() * CHUNK + r];
         const char* src = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES + ((upos ^ (r & 15)) << 4);
         __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
                          :: "s"(tile + (uint32_t)((ow * 64 + p * NO) * 16)), "v"(src) : "memory");
@@ -759,25 +821,30 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   };
 
   // ---- stream cursors (uniform and identical in every wave) ------------------
-  // Score cursor (j, c) of item j's chunk c with nj chunks; the fetch cursor is
-  // one chunk ahead of it.
-  int j = 0, c = 0, nj = chunks_of(0);
-  auto advance = [&](int& jj, int& cc, int& nn) -> bool {  // false at the end of the stream
-    if (++cc < nn) return true;
-    ++jj;
-    cc = 0;
-    if (jj >= J) return false;
-    nn = chunks_of(jj);
-    return true;
-  };
-  // First fetch: chunk (0, 0) into tile 0.
+  // The score cursor; the output waves' fetch cursor runs AHEAD chunks ahead.
+  Cursor cur;
+  start(cur, 0);
+  Cursor fcur = cur;
+  bool fvalid = true;         // fcur is inside the stream
+  bool ahead_loaded = false;  // the last fetch issued is a chunk after the next one consumed
   if (!scorer) {
-    if constexpr (ROW_LOADS) read_entries(0, 0);
-    int j1 = 0, c1 = 0, n1 = nj;
-    const bool v1 = advance(j1, c1, n1);
-    fetch(0, 0, 0, v1, j1, c1);
-    // Q has landed once at most the PIECES loads of the fetch are in flight.
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+    if constexpr (ROW_LOADS) read_entries(fcur);
+    int issued = 0;
+#pragma unroll
+    for (int k = 0; k < AHEAD; ++k) {
+      if (fvalid) {
+        fetch(k, fcur);
+        ++issued;
+        fvalid = advance(fcur);
+        if (ROW_LOADS && fvalid) read_entries(fcur);
+      }
+    }
+    ahead_loaded = issued > 1;
+    // Q has landed once at most the loads of the prologue fetches are in flight.
+    if (issued > 1)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * PIECES) & 15) | (((2 * PIECES) >> 4) << 14));
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
   } else {
     __builtin_amdgcn_s_waitcnt(0x0F70);
   }
@@ -800,22 +867,22 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
     float sink = a.sinks[item_head0(0) + 16 * wave + i16] * LOG2E, sink_next = 0.f;
     float m_run = 0.f, l_run = 0.f;
     for (int s = 0;; ++s) {
-      if (j >= J) {  // stream done: one more barrier for the last PV, then leave
+      if (cur.j >= J) {  // stream done: one more barrier for the last PV, then leave
         block_barrier();
         break;
       }
       block_barrier();
-      if (c == 0) {
-        if (j > 0) {
+      if (cur.c == 0) {
+        if (cur.j > 0) {
 #pragma unroll
           for (int k = 0; k < QK_STEPS; ++k) qf[k] = qf_next[k];
           sink = sink_next;
         }
         m_run = sink;
-        l_run = g == 0 ? 1.0f : 0.0f;  // e^(sink - m) counted once per head
-        if (j + 1 < J) {
-          const int head = item_head0(j + 1) + 16 * wave + i16;
-          const scalar* q_row = (const scalar*)a.q + ((size_t)item_token(j + 1) * a.H + head) * D + 8 * g;
+        l_run = (g == 0 && item_part(cur.j) == 0) ? 1.0f : 0.0f;  // e^(sink - m), once per head
+        if (cur.j + 1 < J) {
+          const int head = item_head0(cur.j + 1) + 16 * wave + i16;
+          const scalar* q_row = (const scalar*)a.q + ((size_t)item_token(cur.j + 1) * a.H + head) * D + 8 * g;
 #pragma unroll
           for (int k = 0; k < QK_STEPS; ++k) qf_next[k] = *(const x8*)(q_row + 32 * k);
           sink_next = a.sinks[head] * LOG2E;
@@ -847,7 +914,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       const int slot = s & 1;
       float x0[4], x1[4];
       float cmax = -INFINITY;
-      const int live = count_lds[j % LISTS] - c * CHUNK;
+      // Rows of this chunk that hold selected entries (<= 0: masked placeholder).
+      const int live = cur.n > 0 ? count_lds[cur.j % LISTS] - (cur.first + cur.c) * CHUNK : 0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         x0[k] = s0[k];
@@ -882,11 +950,14 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       }
       l_run += psum;
       p_lds[slot][wave][lane] = __builtin_bit_cast(u32x4, p8);
-      if (c == nj - 1) {
+      if (cur.c == cur.chunks() - 1) {
         const float l = sum_over_lane_groups(l_run);
-        if (g == 0) linv_lds[j & 1][16 * wave + i16] = 1.0f / l;
+        if (g == 0) {
+          ml_lds[cur.j & 1][0][16 * wave + i16] = m_run;
+          ml_lds[cur.j & 1][1][16 * wave + i16] = l;
+        }
       }
-      advance(j, c, nj);
+      advance(cur);
     }
   } else {
     // ---- output waves: fetch, then O^T[features, heads] += V^T * P^T ----------
@@ -898,25 +969,66 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
 #pragma unroll
     for (int b = 0; b < NB; ++b)
       tr_base[b] = (uint32_t)(rt * ROW_BYTES + (((dbase / 8 + 2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
-    int oj = -1, oc = 0, onj = 0;  // output cursor: the score cursor of the previous step
-    for (int s = 0;; ++s) {
-      const bool score_active = j < J;
-      if (!score_active && oj < 0) break;
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      block_barrier();
-      if (score_active) {
-        // Fetch the chunk after (j, c), and read the entries of the one after that.
-        int j1 = j, c1 = c, n1 = nj;
-        if (advance(j1, c1, n1)) {
-          int j2 = j1, c2 = c1, n2 = n1;
-          const bool v2 = advance(j2, c2, n2);
-          fetch(s + 1, j1, c1, v2, j2, c2);
+
+    // Output of item j: this lane holds heads head0 + 16ht + i16, features
+    // dbase + 16t + 4g + i. A whole item stores O / l; a part stores its
+    // record (O as f32x4 at (ht * PVT + t) * 64 + lane, then m[BMH], l[BMH]).
+    auto finish = [&](int j) {
+      const int key = item_key(j), par = j & 1;
+      if (item_parts(j) == 1) {
+        const int token = key / head_tiles, head0 = (key % head_tiles) * a.BM;
+#pragma unroll
+        for (int ht = 0; ht < NQ; ++ht) {
+          const float inv = 1.0f / ml_lds[par][1][16 * ht + i16];
+          scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + 16 * ht + i16) * D + dbase + 4 * g;
+#pragma unroll
+          for (int t = 0; t < PVT; ++t) {
+            x4 v;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
+            *(x4*)(out_row + 16 * t) = v;
+          }
         }
-        if (c == 0 && j + LISTS - 1 < J) copy_list(j + LISTS - 1);
+        return;
       }
-      if (oj >= 0) {
+      float* rec = a.partials + (((size_t)(key - S0) * P + item_part(j)) * NP + ow) * REC;
+#pragma unroll
+      for (int ht = 0; ht < NQ; ++ht)
+#pragma unroll
+        for (int t = 0; t < PVT; ++t) *(f32x4*)(rec + ((ht * PVT + t) * 64 + lane) * 4) = o[ht][t];
+      if (lane < BMH) {
+        rec[BMH * DPV + lane] = ml_lds[par][0][lane];
+        rec[BMH * DPV + BMH + lane] = ml_lds[par][1][lane];
+      }
+    };
+
+    Cursor ocur = cur;   // output cursor: the score cursor of the previous step
+    bool ovalid = false;
+    bool stored = false;  // the previous step issued global stores
+    for (int s = 0;; ++s) {
+      const bool score_active = cur.j < J;
+      if (!score_active && !ovalid) break;
+      // KV(s) has landed once at most the younger fetch batch is in flight
+      // (stores and loads may complete out of order: wait for all after stores).
+      if (stored || !ahead_loaded)
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+      block_barrier();
+      stored = false;
+      ahead_loaded = false;
+      if (score_active) {
+        if (cur.c == 0 && cur.j + LISTS - 1 < J) copy_list(cur.j + LISTS - 1);
+        if (fvalid) {
+          fetch(s + AHEAD, fcur);
+          fvalid = advance(fcur);
+          if (ROW_LOADS && fvalid) read_entries(fcur);
+          ahead_loaded = AHEAD > 1;
+        }
+      }
+      if (ovalid) {
         const int slot = (s - 1) & 1;
-        if (oc == 0) {
+        if (ocur.c == 0) {
 #pragma unroll
           for (int ht = 0; ht < NQ; ++ht)
 #pragma unroll
@@ -954,33 +1066,97 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
           for (int ht = 0; ht < NQ; ++ht) o[ht][t] = B16<DT>::mfma(v, pb[ht], o[ht][t]);
           __builtin_amdgcn_sched_barrier(0);
         }
-        if (oc == onj - 1) {
-          // Normalise and store item oj: this lane holds head head0 + 16ht +
-          // i16, features dbase + 16t + 4g + i.
-          const int token = item_token(oj), head0 = item_head0(oj);
-#pragma unroll
-          for (int ht = 0; ht < NQ; ++ht) {
-            const float inv = linv_lds[oj & 1][16 * ht + i16];
-            scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + 16 * ht + i16) * D + dbase + 4 * g;
-#pragma unroll
-            for (int t = 0; t < PVT; ++t) {
-              x4 v;
-#pragma unroll
-              for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
-              *(x4*)(out_row + 16 * t) = v;
-            }
-          }
+        if (ocur.c == ocur.chunks() - 1) {
+          finish(ocur.j);
+          stored = true;
         }
       }
       if (score_active) {
-        oj = j;
-        oc = c;
-        onj = nj;
-        advance(j, c, nj);
+        ocur = cur;
+        ovalid = true;
+        advance(cur);
       } else {
-        oj = -1;
+        ovalid = false;
       }
     }
+  }
+}
+
+// Merge of split work items. A record (one per split key, part and output
+// wave ow) holds that wave's O slice as f32x4 at (ht * PVT + t) * 64 + lane
+// (head 16 ht + (lane & 15), features ow * D/NP + 16 t + 4 (lane >> 4) + 0..3),
+// then the running max (log2 units) and denominator of its BM heads. One
+// workgroup per (split key, ow, ht) slice of 16 heads, each thread issuing all
+// of its parts' loads at once, combines the parts in part order
+// (deterministic):
+//   M = max_p m_p, w_p = 2^(m_p - M), O = (sum_p w_p O_p) / (sum_p w_p l_p),
+// the online-softmax merge of attention.py:398-525's running max/denominator
+// over disjoint row sets (the sink's term is in part 0's denominator).
+template <int D, int NP>
+constexpr int merge_threads() {  // threads per 16-head slice: at most 256
+  return (D / NP / 16) * 64 < 256 ? (D / NP / 16) * 64 : 256;
+}
+template <int DT, int D, int NQ, int NP>
+__global__ __launch_bounds__((merge_threads<D, NP>())) void sparse_merge_kernel(SparseArgs a) {
+  typedef typename B16<DT>::scalar scalar;
+  typedef typename B16<DT>::x4 x4;
+  constexpr int BMH = 16 * NQ;
+  constexpr int DPV = D / NP;
+  constexpr int PVT = DPV / 16;
+  constexpr int REC = BMH * DPV + 2 * BMH;
+  constexpr int MT = merge_threads<D, NP>();
+  constexpr int PER = PVT * 64 / MT;  // f32x4 of a 16-head slice per thread
+  static_assert(PVT * 64 % MT == 0 && PER >= 1 && PER <= 4, "slice must split evenly over the threads");
+  const int slice = (int)blockIdx.x % (NP * NQ), split_key = (int)blockIdx.x / (NP * NQ);
+  const int ow = slice / NQ, ht = slice % NQ;
+  const int head_tiles = a.H / a.BM;
+  const int key = a.split_from + split_key;
+  const int token = key / head_tiles, head0 = (key % head_tiles) * a.BM;
+  const int P = a.parts;
+  const size_t part_stride = (size_t)NP * REC;
+  const float* records = a.partials + ((size_t)split_key * P * NP + ow) * REC;
+  // Thread tid holds f32x4 number ht * PVT * 64 + k * MT + tid of the O
+  // slice: tile t = (k * MT + tid) / 64, lane = tid % 64.
+  const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
+  const int h = 16 * ht + i16;
+  float mq[MAX_PARTS], lq[MAX_PARTS];
+  f32x4 oq[MAX_PARTS][PER];
+#pragma unroll
+  for (int q = 0; q < MAX_PARTS; ++q) {
+    if (q < P) {
+      const float* rec = records + q * part_stride;
+      mq[q] = rec[BMH * DPV + h];
+      lq[q] = rec[BMH * DPV + BMH + h];
+#pragma unroll
+      for (int k = 0; k < PER; ++k) oq[q][k] = *(const f32x4*)(rec + (ht * PVT * 64 + k * MT + threadIdx.x) * 4);
+    }
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < MAX_PARTS; ++q)
+    if (q < P) M = fmaxf(M, mq[q]);
+  float L = 0.f;
+  f32x4 acc[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < MAX_PARTS; ++q) {
+    if (q < P) {
+      const float w = fast_exp2(mq[q] - M);
+      L += lq[q] * w;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) acc[k] += oq[q][k] * w;
+    }
+  }
+  const float inv = 1.0f / L;
+  scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + h) * D + ow * DPV + 4 * g;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int t = (k * MT + (int)threadIdx.x) / 64;
+    x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (scalar)(acc[k][e] * inv);
+    *(x4*)(out_row + 16 * t) = v;
   }
 }
 
@@ -1024,8 +1200,41 @@ static int check_sparse(const SparseMlaParams* p) {
   if ((int64_t)p->ORI_BLOCKS * p->PAGE >= (int64_t)CMP_BIT) return AFA_E_SHAPE;
   if ((int64_t)p->CMP_BLOCKS * (p->PAGE / p->RATIO) >= (int64_t)CMP_BIT) return AFA_E_SHAPE;
   if (!(p->scale > 0.0f)) return AFA_E_SHAPE;
-  if ((int64_t)p->T * (p->H / p->BM) > 0x7fffffffLL) return AFA_E_SHAPE;
+  if (p->parts < 0 || p->parts > MAX_PARTS) return AFA_E_SHAPE;
+  if ((int64_t)p->T * (p->H / p->BM) * MAX_PARTS > 0x7fffffffLL) return AFA_E_SHAPE;
   return AFA_OK;
+}
+
+// Split of the (token, BM-head tile) keys for the persistent kernel. With R
+// full rounds of 256 keys (a fixed model of MI355X's 256 compute units keeps
+// the workspace size a function of the sizes alone) and r keys left over, the
+// last round would keep only r CUs busy for a whole key's chunks. Splitting
+// those r keys into P = min(MAX_PARTS, 256 / r) parts gives every CU at most
+// one part in that round. The plan kernel, the parts' FP32 records and the
+// merge kernel cost about MERGE_COST chunk steps (measured on decode B64 x 6:
+// plan 6.7 us + merge 8.5 us, ~1.5 us per chunk step), so a split is taken only
+// where it shortens the longest stream by more: small batches (T = 16: 3 chunk
+// steps + merge instead of 20), not decode B64 x 6 (20 + 10 + merge against
+// 40). parts = 1 never splits; parts > 1 splits every key into that many parts.
+struct Split {
+  int parts;           // parts of each split key (1: nothing split)
+  int64_t split_from;  // first split key
+};
+constexpr int64_t SPLIT_MODEL_CUS = 256;
+constexpr int64_t MERGE_COST = 10;
+static Split choose_split(const SparseMlaParams* p) {
+  const int64_t tiles = (int64_t)p->T * (p->H / p->BM);
+  if (p->parts == 1) return Split{1, tiles};
+  if (p->parts > 1) return Split{p->parts, 0};
+  const int64_t nch = std::max<int64_t>(1, (p->WINDOW + p->TOPK + CHUNK - 1) / CHUNK);
+  const int64_t rounds = tiles / SPLIT_MODEL_CUS, rest = tiles % SPLIT_MODEL_CUS;
+  if (rest == 0) return Split{1, tiles};
+  const int parts = (int)std::min<int64_t>(std::min<int64_t>(MAX_PARTS, SPLIT_MODEL_CUS / rest), nch);
+  if (parts < 2) return Split{1, tiles};
+  const int64_t whole = (rounds + 1) * nch;
+  const int64_t split = rounds * nch + (nch + parts - 1) / parts + MERGE_COST;
+  if (split >= whole) return Split{1, tiles};
+  return Split{parts, rounds * SPLIT_MODEL_CUS};
 }
 
 static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void* ori_kv,
@@ -1064,16 +1273,32 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   a.list_pad = (p->WINDOW + p->TOPK + 255) / 256 * 256;
   a.plan_rows = nullptr;
   a.plan_count = nullptr;
+  a.partials = nullptr;
+  const Split split = choose_split(p);
+  a.parts = split.parts;
+  a.split_from = (int32_t)split.split_from;
   a.scale = p->scale;
   return a;
 }
 
-// Plan workspace: [T] counts (rounded up to 256 bytes), then [T][list_pad]
-// row lists.
-static size_t plan_count_bytes(int64_t T) { return (size_t)((T * 4 + 255) / 256 * 256); }
-static size_t plan_bytes(const SparseMlaParams* p) {
+// Plan workspace, each slice starting on a 256-byte boundary:
+//   [T] counts | [T][list_pad] row lists | partial records of split keys,
+//   [split keys][parts][BM / 16 output waves][BM * D / (BM / 16) + 2 * BM]
+//   floats: per (key, part) BM * D + BM * BM / 8 floats (each output wave's
+//   O slice, and the running max and denominator of every head).
+static size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+static size_t plan_count_bytes(int64_t T) { return round256((size_t)T * 4); }
+static size_t plan_rows_bytes(const SparseMlaParams* p) {
   const int64_t list_pad = (p->WINDOW + p->TOPK + 255) / 256 * 256;
-  return plan_count_bytes(p->T) + (size_t)p->T * (size_t)list_pad * 4;
+  return (size_t)p->T * (size_t)list_pad * 4;
+}
+static size_t partial_bytes(const SparseMlaParams* p, const Split& split) {
+  const int64_t tiles = (int64_t)p->T * (p->H / p->BM);
+  if (split.parts < 2) return 0;
+  return (size_t)(tiles - split.split_from) * (size_t)split.parts * (size_t)(p->BM * p->D + p->BM * p->BM / 8) * 4;
+}
+static size_t plan_bytes(const SparseMlaParams* p) {
+  return round256(plan_count_bytes(p->T) + plan_rows_bytes(p)) + partial_bytes(p, choose_split(p));
 }
 
 // LDS of one workgroup (the KV ring, P slots and the row list) must fit the
@@ -1099,23 +1324,39 @@ template <int DT, int D, int NQ, int NP>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
   if (a.plan_rows != nullptr) {
-    // Plan kernel, then the persistent kernel over the plan (four row lists)
-    // when every CU gets at least two items (it removes the per-item start,
-    // which outweighs a second kernel only then) and four lists fit next to
-    // its ring. Otherwise the one-item-per-workgroup kernel resolves its rows.
+    // Plan kernel, then the persistent kernel over the plan when keys are
+    // split into parts or every CU gets at least two items (the persistent
+    // form removes the per-item start, which outweighs a second kernel only
+    // then) and its row-list ring fits next to its KV ring, then the merge of
+    // split keys. Short streams (at most four items per CU, rows mostly from
+    // HBM) use a 4-tile ring with two chunks in flight, long ones 3 tiles.
+    // Otherwise the one-item-per-workgroup kernel resolves its rows.
     static int cus = 0;
     if (cus == 0) cus = device_cus();
-    const int64_t items = (int64_t)a.T * (a.H / a.BM);
-    const size_t lists = 4 * lds;
-    if (items >= 2 * (int64_t)cus &&
-        fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP>, lists) == AFA_OK) {
-      constexpr int PLAN_THREADS = 256;
-      hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return (int)e;
-      hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP>), dim3((unsigned)cus),
-                         dim3((NQ + NP) * 64), lists, stream, a);
-      return (int)hipGetLastError();
+    const int64_t tiles = (int64_t)a.T * (a.H / a.BM);
+    const int64_t items = a.split_from + (tiles - a.split_from) * a.parts;
+    if (a.parts > 1 || items >= 2 * (int64_t)cus) {
+      const int64_t per_cu = (items + cus - 1) / cus;
+      const bool deep = per_cu <= 4 && fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>, 5 * lds) == AFA_OK;
+      if (deep || fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>, 4 * lds) == AFA_OK) {
+        constexpr int PLAN_THREADS = 256;
+        hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+        const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
+        if (deep)
+          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>), dim3(grid), dim3((NQ + NP) * 64),
+                             5 * lds, stream, a);
+        else
+          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64),
+                             4 * lds, stream, a);
+        if (a.parts < 2) return (int)hipGetLastError();
+        const hipError_t e2 = hipGetLastError();
+        if (e2 != hipSuccess) return (int)e2;
+        hipLaunchKernelGGL((sparse_merge_kernel<DT, D, NQ, NP>), dim3((unsigned)((tiles - a.split_from) * NP * NQ)),
+                           dim3(merge_threads<D, NP>()), 0, stream, a);
+        return (int)hipGetLastError();
+      }
     }
   }
   const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
@@ -1157,8 +1398,13 @@ extern "C" int launch_sparse_mla(void* stream, const void* q, const void* ori_kv
   // With a workspace the row lists come from the plan kernel; the debug image
   // is written by the fused setup, so a debug call resolves rows in place.
   if (workspace != nullptr && params->debug_rows == nullptr) {
-    a.plan_count = (int32_t*)workspace;
-    a.plan_rows = (uint32_t*)((char*)workspace + plan_count_bytes(params->T));
+    char* w = (char*)workspace;
+    a.plan_count = (int32_t*)w;
+    a.plan_rows = (uint32_t*)(w + plan_count_bytes(params->T));
+    if (a.parts > 1) a.partials = (float*)(w + round256(plan_count_bytes(params->T) + plan_rows_bytes(params)));
+  } else {
+    a.parts = 1;
+    a.split_from = a.T * (a.H / a.BM);
   }
   hipStream_t s = (hipStream_t)stream;
   return params->dtype == AFA_DTYPE_BF16 ? dispatch_d<DT_BF16>(a, s) : dispatch_d<DT_F16>(a, s);

@@ -37,7 +37,8 @@ def check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PA
     require(D in (128, 256, 512), "gfx950 kernel supports D in {128, 256, 512}")
 
 
-def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows=None):
+def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows=None,
+                parts=0):
     return _native.SparseMlaParams(
         B=B,
         T=T,
@@ -54,7 +55,7 @@ def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW
         BM=BM,
         dtype=_native.AFA_DTYPE[dtype],
         scale=SCALE,
-        reserved=0,
+        parts=parts,
         debug_rows=None if debug_rows is None else debug_rows.data_ptr(),
     )
 
@@ -125,12 +126,19 @@ def sparse_mla(
     SCALE=0.04419417382415922,
     *,
     debug_rows=None,
+    parts=None,
 ):
     """Sparse MLA forward; writes ``attention_out`` [T, H, D] and returns it.
 
     ``debug_rows`` (optional int32 [T, S, 2] device tensor) receives the
     kernel's own row selection per gather slot: (cache, physical row),
     cache 0 = ori_kv, 1 = cmp_kv, (-1, -1) unused.
+
+    ``parts`` (optional, 1..8) fixes how many workgroups share one token's
+    selected rows on the plan path: 1 never splits, k > 1 splits every token
+    into k parts whose partial results a merge kernel combines. By default only
+    the tokens of an incomplete last round over the 256 CUs are split, where
+    that shortens the longest per-CU stream (decode-sized batches).
     """
     dtype = storage_dtype(DTYPE)
     check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PARTS, GROUPS, VR, BK, C, SCALE)
@@ -155,7 +163,9 @@ def sparse_mla(
     )
     if debug_rows is not None:
         check_tensor("debug_rows", debug_rows, (T, S, 2), torch.int32, device)
-    params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows)
+    require(parts is None or parts in range(1, 9), "parts must be None or 1..8")
+    params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows,
+                         parts or 0)
     lib = _native.library()
     # The workspace holds the per-token row-list plan (see workspace_size_sparse_mla);
     # the caching allocator hands it out in stream order, so no host sync.

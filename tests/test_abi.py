@@ -44,12 +44,36 @@ def test_kernel_config_and_workspace_queries(lib):
     size = ct.c_uint64(123)
     # The sparse workspace is the row-list plan: T counts rounded up to 256
     # bytes, then T lists of WINDOW + TOPK entries rounded up to 256.
-    params = good_params()
+    params = good_params(parts=1)
     assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
     assert size.value == 256 + 16 * 768 * 4
-    params = good_params(T=100, TOPK=1000, S=1128)
+    params = good_params(T=100, TOPK=1000, S=1128, parts=1)
     assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
     assert size.value == 512 + 100 * 1280 * 4
+    # Split keys add partial records: (split keys) * P * (BM * D + BM * BM / 8)
+    # floats. Automatically only the keys of an incomplete last round of 256
+    # are split, into min(8, 256 / leftover) parts, and only where that saves
+    # more than the merge's cost of 10 chunk steps: T = 16 (no full round) into
+    # 8 parts, T = 100 with 36 chunks into 2; not decode T = 384 (20 + 10 + 10
+    # against 40 chunk steps) nor T = 512 (two full rounds).
+    per_part = (64 * 512 + 64 * 64 // 8) * 4
+    params = good_params()
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
+    assert size.value == 49408 + 16 * 8 * per_part
+    params = good_params(T=100, TOPK=1000, S=1128)
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
+    assert size.value == 512512 + 100 * 2 * per_part
+    params = good_params(T=384)
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
+    assert size.value == 1536 + 384 * 768 * 4
+    params = good_params(T=512)
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
+    assert size.value == 2048 + 512 * 768 * 4
+    params = good_params(T=512, parts=3)  # forced: every key in 3 parts
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
+    assert size.value == 2048 + 512 * 768 * 4 + 512 * 3 * per_part
+    for parts in (-1, 9):
+        assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(good_params(parts=parts))) == -2
     assert lib.workspace_size_sparse_mla(ct.byref(size), None) == -1
     assert lib.workspace_size_sparse_mla(None, None) == -1
     assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(good_params(D=64))) == -2
@@ -68,7 +92,7 @@ def test_sparse_metadata_lists_tensors_in_reference_order(lib):
 
 def good_params(**overrides):
     fields = dict(B=4, T=16, H=64, D=512, PAGE=128, RATIO=2, MAX_SEQ=4096, ORI_BLOCKS=128, CMP_BLOCKS=128,
-                  WINDOW=128, TOPK=512, S=640, BM=64, dtype=0, scale=0.044, reserved=0, debug_rows=None)
+                  WINDOW=128, TOPK=512, S=640, BM=64, dtype=0, scale=0.044, parts=0, debug_rows=None)
     fields.update(overrides)
     return _native.SparseMlaParams(**fields)
 

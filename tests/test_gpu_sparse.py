@@ -60,29 +60,43 @@ def test_validation_cases_match_oracle(device, case, variant):
     np.testing.assert_array_equal(bias, bias_ref)
     np.testing.assert_array_equal(kv, kv_ref)
     actual = tensors["attention_out"].float().cpu().numpy()
-    assert_close(actual, sr.oracle_fp32(data, policy), policy["DTYPE"])
+    ref = sr.oracle_fp32(data, policy)
+    assert_close(actual, ref, policy["DTYPE"])
     if case == "empty":
         assert np.all(actual == 0)
-    # Without the debug image the call gets a plan workspace; at this size
-    # (fewer than two work items per CU) it still resolves rows in-kernel, and
-    # must give the same bits. The persistent test below covers the plan path.
+    # Without the debug image the call gets a plan workspace. With one part at
+    # this size (fewer than two work items per CU) rows are still resolved
+    # in-kernel: the same bits. By default (None) the library splits each token
+    # over eight workgroups here (no full round of 256 tiles: plan, persistent
+    # and merge kernels); 2, 3 and 8 parts cover other merge widths, with
+    # masked placeholder parts where a token has fewer chunks than parts.
     from ascendflow_amd.sparse_attention import sparse_mla
 
     fused = tensors["attention_out"].clone()
-    tensors["attention_out"].fill_(float("nan"))
-    sparse_mla(*call_args(tensors), **call_kwargs(policy))
-    torch.cuda.synchronize()
-    assert torch.equal(fused, tensors["attention_out"]), "the call without the debug image differs"
-    assert guard_intact(tensors), "kernel wrote past attention_out"
+    for parts in (1, None, 2, 3, 8):
+        tensors["attention_out"].fill_(float("nan"))
+        sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=parts)
+        torch.cuda.synchronize()
+        assert guard_intact(tensors), f"kernel wrote past attention_out (parts={parts})"
+        if parts == 1:
+            assert torch.equal(fused, tensors["attention_out"]), "the call without the debug image differs"
+            continue
+        split = tensors["attention_out"].float().cpu().numpy()
+        assert_close(split, ref, policy["DTYPE"])
+        if case == "empty":
+            assert np.all(split == 0), f"empty selection not zero with parts={parts}"
 
 
 @pytest.mark.parametrize("variant", [v for v in VARIANTS if "topk" not in v])
 def test_persistent_stream_matches_fused_and_oracle(device, variant):
     """T = 544 tokens: at least two work items per CU, so the plan path runs
     the persistent kernel, whose workgroups stream many tokens (and, with
-    BM = 32, both head tiles of a token) through one pipeline. Its output must
-    equal the in-kernel row resolution bit for bit, and the oracle on a sample
-    that includes empty and one-row selections."""
+    BM = 32, both head tiles of a token) through one pipeline. With one part
+    its output must equal the in-kernel row resolution bit for bit; with the
+    tokens split over 2 or 4 workgroups (partial results merged, 3-tile ring)
+    it must match the oracle on a sample that includes empty and one-row
+    selections. By default (None) the 32 (BM = 64) or 64 (BM = 32) tiles of
+    the incomplete third or fifth round are split and merged."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
     policy = sr.default_policy(B=6, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
@@ -93,15 +107,23 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
     torch.cuda.synchronize()
     fused = tensors["attention_out"].clone()
     tensors["attention_out"].fill_(float("nan"))
-    sparse_mla(*call_args(tensors), **call_kwargs(policy))
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1)
     torch.cuda.synchronize()
     assert guard_intact(tensors), "kernel wrote past attention_out"
     assert torch.equal(fused, tensors["attention_out"]), "persistent stream differs from the in-kernel row resolution"
     rows = (debug[..., 0] >= 0).sum(dim=1).cpu().numpy()
     rng = np.random.default_rng(11)
     tokens = sorted({0, 1, 543, *np.flatnonzero(rows <= 1)[:8].tolist(), *rng.choice(544, 24, replace=False).tolist()})
-    actual = tensors["attention_out"][torch.as_tensor(tokens, device=device)].float().cpu().numpy()
-    assert_close(actual, sr.oracle_fp32(data, policy, tokens), policy["DTYPE"])
+    index = torch.as_tensor(tokens, device=device)
+    ref = sr.oracle_fp32(data, policy, tokens)
+    assert_close(tensors["attention_out"][index].float().cpu().numpy(), ref, policy["DTYPE"])
+    for parts in (None, 2, 4):
+        tensors["attention_out"].fill_(float("nan"))
+        sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=parts)
+        torch.cuda.synchronize()
+        assert guard_intact(tensors), f"kernel wrote past attention_out (parts={parts})"
+        assert torch.isfinite(tensors["attention_out"].float()).all(), f"unwritten output (parts={parts})"
+        assert_close(tensors["attention_out"][index].float().cpu().numpy(), ref, policy["DTYPE"])
 
 
 def test_relaunch_is_bitwise_deterministic(device):
@@ -118,9 +140,12 @@ def test_relaunch_is_bitwise_deterministic(device):
     assert torch.equal(first, tensors["attention_out"])
 
 
-def check_measured(inputs, tokens, device):
+def check_measured(inputs, tokens, device, split=False):
     """Runs without the debug image first (the path the benchmark takes), then
-    with it; the debug dump must not change any output bit, for every token."""
+    with it (in-kernel row resolution, one part per token). Unless the plan
+    path splits tokens into parts (``split``: the merge sums in another
+    order), the debug dump must not change any output bit; both outputs must
+    match the oracle, and the debug image the oracle's selection."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
     policy = inputs.policy
@@ -130,12 +155,15 @@ def check_measured(inputs, tokens, device):
     debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
     sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), debug_rows=debug)
     torch.cuda.synchronize()
-    assert torch.equal(plain, inputs.tensors["attention_out"]), "the debug image changed the output"
+    if not split:
+        assert torch.equal(plain, inputs.tensors["attention_out"]), "the debug image changed the output"
     data = host_view(inputs, tokens)
     index = torch.as_tensor(tokens, device=device)
     np.testing.assert_array_equal(debug[index].cpu().numpy(), expected_rows(data, policy, tokens))
+    ref = sr.oracle_fp32(data, policy, tokens)
+    assert_close(plain[index].float().cpu().numpy(), ref, policy["DTYPE"])
     actual = inputs.tensors["attention_out"][index].float().cpu().numpy()
-    return assert_close(actual, sr.oracle_fp32(data, policy, tokens), policy["DTYPE"])
+    return assert_close(actual, ref, policy["DTYPE"])
 
 
 def test_decode_b64x6_ctx128k_all_tokens(device):
@@ -146,6 +174,16 @@ def test_decode_b64x6_ctx128k_all_tokens(device):
     policy = measurement_policy(batch=64, query_tokens=6, context=131072)
     inputs = make_inputs(policy, 131072, device=device)
     check_measured(inputs, list(range(policy["T"])), device)
+    # Forced split: every token over two workgroups, partial results merged.
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    plain = inputs.tensors["attention_out"].clone()
+    sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), parts=2)
+    torch.cuda.synchronize()
+    split = inputs.tensors["attention_out"].float()
+    err = (split - plain.float()).abs().max().item()
+    assert err <= 1e-2 * plain.float().abs().max().item(), f"split decode differs by {err}"
+
 
 
 def test_prefill_q8k_ctx32k_sampled_tokens(device):
