@@ -60,6 +60,7 @@ class SparseMlaParams(ct.Structure):
         ("scale", ct.c_float),
         ("parts", ct.c_int32),
         ("debug_rows", ct.c_void_p),
+        ("softmax_lse", ct.c_void_p),
     ]
 
 

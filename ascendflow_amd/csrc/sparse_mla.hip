@@ -42,6 +42,12 @@ constexpr int CHUNK = 32;                 // rows per LDS stage
 constexpr int MAX_PARTS = 8;              // most parts a token's chunk list is split into
 constexpr uint32_t CMP_BIT = 0x80000000u; // row-list tag: row lives in cmp_kv
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+// Natural-log normaliser of a head's softmax: ln(sum_j e^(s_j) + e^sink), from
+// the running max m (log2 units, scores pre-scaled by log2 e) and the
+// denominator l relative to it.
+__device__ __forceinline__ float lse_of(float m, float l) { return (m + __log2f(l)) * LN2; }
 
 struct SparseArgs {
   const void* q;
@@ -57,6 +63,7 @@ struct SparseArgs {
   const int32_t* ori_topk_length;
   const float* sinks;
   void* out;
+  float* lse;            // optional [T][H] natural-log softmax normaliser, or null
   int32_t* debug_rows;
   uint32_t* plan_rows;   // workspace: [T][list_pad] padded row lists, or null
   int32_t* plan_count;   // workspace: [T] selected rows per token
@@ -545,7 +552,10 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       p_lds[slot][wave][lane] = __builtin_bit_cast(u32x4, p8);
     }
     const float l = sum_over_lane_groups(l_run);
-    if (g == 0) linv_lds[16 * wave + i16] = 1.0f / l;
+    if (g == 0) {
+      linv_lds[16 * wave + i16] = 1.0f / l;
+      if (a.lse != nullptr) a.lse[(size_t)token * a.H + qhead] = lse_of(m_run, l);
+    }
     __syncthreads();
   } else {
     // ---- 4b. output wave: O^T[features, heads] += V^T * P^T ------------------
@@ -955,6 +965,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
         if (g == 0) {
           ml_lds[cur.j & 1][0][16 * wave + i16] = m_run;
           ml_lds[cur.j & 1][1][16 * wave + i16] = l;
+          if (a.lse != nullptr && item_parts(cur.j) == 1)
+            a.lse[(size_t)item_token(cur.j) * a.H + item_head0(cur.j) + 16 * wave + i16] = lse_of(m_run, l);
         }
       }
       advance(cur);
@@ -1149,6 +1161,7 @@ __global__ __launch_bounds__((merge_threads<D, NP>())) void sparse_merge_kernel(
     }
   }
   const float inv = 1.0f / L;
+  if (a.lse != nullptr && ow == 0 && threadIdx.x < 16) a.lse[(size_t)token * a.H + head0 + h] = lse_of(M, L);
   scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + h) * D + ow * DPV + 4 * g;
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
@@ -1256,6 +1269,7 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   a.ori_topk_length = otl;
   a.sinks = sinks;
   a.out = out;
+  a.lse = p->softmax_lse;
   a.debug_rows = p->debug_rows;
   a.B = p->B;
   a.T = p->T;

@@ -2,5 +2,6 @@
 
 from .attention import sparse_mla
 from .gather import sparse_mla_gather
+from .ops import sparse_flash_mla
 
-__all__ = ["sparse_mla", "sparse_mla_gather"]
+__all__ = ["sparse_mla", "sparse_mla_gather", "sparse_flash_mla"]

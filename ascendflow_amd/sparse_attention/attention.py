@@ -38,7 +38,7 @@ def check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PA
 
 
 def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows=None,
-                parts=0):
+                parts=0, softmax_lse=None):
     return _native.SparseMlaParams(
         B=B,
         T=T,
@@ -57,6 +57,7 @@ def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW
         scale=SCALE,
         parts=parts,
         debug_rows=None if debug_rows is None else debug_rows.data_ptr(),
+        softmax_lse=None if softmax_lse is None else softmax_lse.data_ptr(),
     )
 
 
@@ -127,12 +128,18 @@ def sparse_mla(
     *,
     debug_rows=None,
     parts=None,
+    softmax_lse=None,
 ):
     """Sparse MLA forward; writes ``attention_out`` [T, H, D] and returns it.
 
     ``debug_rows`` (optional int32 [T, S, 2] device tensor) receives the
     kernel's own row selection per gather slot: (cache, physical row),
     cache 0 = ori_kv, 1 = cmp_kv, (-1, -1) unused.
+
+    ``softmax_lse`` (optional float32 [T, H] device tensor) receives the
+    natural-log normaliser ln(sum_j exp(s_j) + exp(sinks[h])) of every
+    (token, head), i.e. the denominator of ``attention_out`` (the sink alone
+    for an empty selection).
 
     ``parts`` (optional, 1..8) fixes how many workgroups share one token's
     selected rows on the plan path: 1 never splits, k > 1 splits every token
@@ -163,9 +170,12 @@ def sparse_mla(
     )
     if debug_rows is not None:
         check_tensor("debug_rows", debug_rows, (T, S, 2), torch.int32, device)
+    if softmax_lse is not None:
+        check_tensor("softmax_lse", softmax_lse, (T, H), torch.float32, device)
+        check_disjoint([(name, t, False) for name, t in tensors.items()] + [("softmax_lse", softmax_lse, True)])
     require(parts is None or parts in range(1, 9), "parts must be None or 1..8")
     params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows,
-                         parts or 0)
+                         parts or 0, softmax_lse)
     lib = _native.library()
     # The workspace holds the per-token row-list plan (see workspace_size_sparse_mla);
     # the caching allocator hands it out in stream order, so no host sync.

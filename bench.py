@@ -217,7 +217,7 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", *ATTENTION_KEYS], default=None,
+    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", "decode768", *ATTENTION_KEYS], default=None,
                         help="time one configuration only (profiling runs; the attention keys print a log only)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-attention", action="store_true", help="skip the flash/teaching attention extras")
@@ -264,8 +264,10 @@ def main():
         "prefill8k": ("sparse_mla prefill B1 Q8192 ctx32768", 1, 8192, 32768),
         "decode": ("sparse_mla decode B64x6 ctx131072", 64, 6, 131072),
         "prefill32k": ("sparse_mla prefill B1 Q32768 ctx32768", 1, 32768, 32768),
+        # README.md:36's second decode row (not a BASELINE config): B128 x 6 at 128K.
+        "decode768": ("sparse_mla decode B128x6 ctx131072", 128, 6, 131072),
     }
-    order = [args.only] if args.only else ["prefill8k", "decode", "prefill32k"]
+    order = [args.only] if args.only else ["prefill8k", "decode", "prefill32k", "decode768"]
     results = {}
     for key in order:
         name, b, q, ctx = configs[key]
@@ -319,7 +321,7 @@ def main():
         },
         "cpu_baseline": {k: v for k, v in baseline.items() if k != "ms_full_scaled"} if baseline else None,
         "extra": {k: {kk: vv for kk, vv in v.items() if kk != "_inputs"} for k, v in results.items()},
-        "reference_ascend_910b3_ms": {"prefill8k": 6.847, "prefill32k": 27.225, "decode": 0.410},
+        "reference_ascend_910b3_ms": {"prefill8k": 6.847, "prefill32k": 27.225, "decode": 0.410, "decode768": 0.810},
     }
     record["extra"].update(extras)
     if baseline:

@@ -62,6 +62,14 @@ typedef struct SparseMlaParams {
    * 1 = cmp_kv, (-1, -1) for an unused slot.  Written by the fused kernel
    * itself, from the same row list it then attends over. */
   int32_t* debug_rows;
+  /* Optional f32 [T, H] output, NULL normally: the natural-log softmax
+   * normaliser ln(sum_j e^(s_j) + e^sink[h]) of each (token, head), s_j =
+   * SCALE * q.k_j over the selected rows (the sink alone for an empty
+   * selection), i.e. the denominator of attention_out. The counterpart of the
+   * softmax_lse output of the vendor operator the reference benchmarks against
+   * (aclnnSparseFlashMla, benchmarks/references/sparse_mla_aclnn.py:100-130),
+   * which the DSL kernel itself does not produce. */
+  float* softmax_lse;
 } SparseMlaParams;
 
 /* Sparse MLA forward: examples/sparse_attention/attention.py:210-525.

@@ -19,6 +19,13 @@ Restates the reference's independent CPU semantics:
   workspace: window slot ``i``, compressed slot ``WINDOW + rank``, bias 0 / -inf).
 - ``oracle``          <- ``sparse_reference.py:127-138`` (FP32 softmax with one sink per
   head in the denominator, output rounded to the storage dtype).
+- ``oracle_lse``      the natural-log softmax normaliser ln(sum_j e^(s_j) + e^sink) per
+  (token, head): the ``softmax_lse`` output of the vendor operator the reference
+  benchmarks against (``benchmarks/references/sparse_mla_aclnn.py:100-130``), i.e. the
+  denominator ``oracle`` divides by. The reference's own kernel has no LSE output, so
+  this is pinned by closed forms (q = 0 gives ln(n + e^sink), an empty selection gives
+  the sink), by scipy's logsumexp over the scores with the sink as one more column, and
+  by rebuilding ``oracle_fp32`` from it.
 - ``inputs``          <- ``sparse_reference.py:45-104`` (the eight validation cases),
   written independently with this repository's own seed use.
 
@@ -169,6 +176,27 @@ def attend(q_token, rows, sinks, scale):
     weights = np.exp(scores - maximum[:, None])
     denominator = weights.sum(axis=1) + np.exp(sinks - maximum)
     return (weights @ rows) / denominator[:, None]
+
+
+def attend_lse(q_token, rows, sinks, scale):
+    """Natural-log softmax normaliser of one token, float64 [H]:
+    ln(sum_j exp(scale * q.k_j) + exp(sink)), the sink alone when nothing is selected."""
+    sinks = np.asarray(sinks, np.float64)
+    if len(rows) == 0:
+        return sinks.copy()
+    scores = (np.asarray(q_token, np.float64) @ np.asarray(rows, np.float64).T) * float(scale)
+    maximum = np.maximum(scores.max(axis=1), sinks)
+    return maximum + np.log(np.exp(scores - maximum[:, None]).sum(axis=1) + np.exp(sinks - maximum))
+
+
+def oracle_lse(data, policy, tokens=None):
+    """Softmax normaliser [len(tokens), H] in float64 (all tokens by default)."""
+    tokens = range(policy["T"]) if tokens is None else tokens
+    out = []
+    for token in tokens:
+        rows, _ = selected_rows(data, policy, token)
+        out.append(attend_lse(data["q"][token], rows, data["sinks"], policy["SCALE"]))
+    return np.stack(out)
 
 
 def oracle_fp32(data, policy, tokens=None):

@@ -150,3 +150,25 @@ def test_python_entries_check_the_reference_asserts_before_launching():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _native.library(tmp_path / "absent.so")
+
+
+def test_framework_op_is_registered_with_a_shape_only_fake():
+    """ascendflow_amd::sparse_flash_mla traces on meta tensors (no GPU, no
+    launch): output [T, H, D] in the query dtype, softmax_lse f32 [T, H] or empty."""
+    import torch
+
+    import ascendflow_amd.sparse_attention  # noqa: F401  registers the op
+
+    meta = torch.device("meta")
+    t, h, d = 6, 64, 512
+    i32 = lambda *shape: torch.empty(*shape, dtype=torch.int32, device=meta)  # noqa: E731
+    args = (torch.empty(t, h, d, dtype=torch.bfloat16, device=meta),
+            torch.empty(32, 128, 1, d, dtype=torch.bfloat16, device=meta),
+            torch.empty(32, 64, 1, d, dtype=torch.bfloat16, device=meta),
+            i32(t, 1, 512), i32(2, 16), i32(2, 16), i32(3), i32(2), i32(2), i32(2), i32(t, 1),
+            torch.empty(h, device=meta), 512 ** -0.5, 2)
+    out, lse = torch.ops.ascendflow_amd.sparse_flash_mla(*args, return_softmax_lse=True)
+    assert out.shape == (t, h, d) and out.dtype == torch.bfloat16
+    assert lse.shape == (t, h) and lse.dtype == torch.float32
+    _, empty = torch.ops.ascendflow_amd.sparse_flash_mla(*args)
+    assert empty.numel() == 0

@@ -29,13 +29,23 @@ VARIANTS = {
 }
 
 
+LSE_RTOL, LSE_ATOL = 1e-4, 1e-3  # FP32 scores from b16 inputs; exp2/log2 of the running sums
+
+
+def assert_lse(actual, ref):
+    actual = actual.cpu().numpy().astype(np.float64)
+    assert np.isfinite(actual).all(), "non-finite softmax_lse"
+    np.testing.assert_allclose(actual, ref, rtol=LSE_RTOL, atol=LSE_ATOL)
+
+
 def run_case(policy, data, device):
     from ascendflow_amd.sparse_attention import sparse_mla, sparse_mla_gather
 
     tensors = to_device(data, policy, device)
     before = {k: tensors[k].clone() for k in sr.TENSOR_ORDER if k != "attention_out"}
     debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
-    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug)
+    tensors["_lse"] = torch.full((policy["T"], policy["H"]), float("nan"), dtype=torch.float32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug, softmax_lse=tensors["_lse"])
     kv, bias = sparse_mla_gather(*(tensors[k] for k in ("ori_kv", "cmp_kv", *INT_KEYS)),
                                  **{k: policy[k] for k in ("B", "T", "D", "PAGE", "RATIO", "MAX_SEQ", "ORI_BLOCKS",
                                                            "CMP_BLOCKS", "WINDOW", "TOPK", "S", "DTYPE")})
@@ -43,6 +53,7 @@ def run_case(policy, data, device):
     assert guard_intact(tensors), "kernel wrote past attention_out"
     for k, v in before.items():
         assert torch.equal(tensors[k], v), f"input {k} changed"
+    assert_lse(tensors["_lse"], sr.oracle_lse(data, policy))
     return tensors, debug.cpu().numpy(), kv.float().cpu().numpy(), bias.cpu().numpy()
 
 
@@ -73,16 +84,21 @@ def test_validation_cases_match_oracle(device, case, variant):
     from ascendflow_amd.sparse_attention import sparse_mla
 
     fused = tensors["attention_out"].clone()
+    fused_lse = tensors["_lse"].clone()
+    lse_ref = sr.oracle_lse(data, policy)
     for parts in (1, None, 2, 3, 8):
         tensors["attention_out"].fill_(float("nan"))
-        sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=parts)
+        tensors["_lse"].fill_(float("nan"))
+        sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=parts, softmax_lse=tensors["_lse"])
         torch.cuda.synchronize()
         assert guard_intact(tensors), f"kernel wrote past attention_out (parts={parts})"
         if parts == 1:
             assert torch.equal(fused, tensors["attention_out"]), "the call without the debug image differs"
+            assert torch.equal(fused_lse, tensors["_lse"]), "softmax_lse differs without the debug image"
             continue
         split = tensors["attention_out"].float().cpu().numpy()
         assert_close(split, ref, policy["DTYPE"])
+        assert_lse(tensors["_lse"], lse_ref)
         if case == "empty":
             assert np.all(split == 0), f"empty selection not zero with parts={parts}"
 
@@ -103,27 +119,35 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
     data = sr.inputs(policy, "mixed")
     tensors = to_device(data, policy, device)
     debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
-    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug)
+    lse = torch.full((policy["T"], policy["H"]), float("nan"), dtype=torch.float32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug, softmax_lse=lse)
     torch.cuda.synchronize()
-    fused = tensors["attention_out"].clone()
+    fused, fused_lse = tensors["attention_out"].clone(), lse.clone()
     tensors["attention_out"].fill_(float("nan"))
-    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1)
+    lse.fill_(float("nan"))
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse)
     torch.cuda.synchronize()
     assert guard_intact(tensors), "kernel wrote past attention_out"
     assert torch.equal(fused, tensors["attention_out"]), "persistent stream differs from the in-kernel row resolution"
+    assert torch.equal(fused_lse, lse), "persistent softmax_lse differs from the in-kernel row resolution"
     rows = (debug[..., 0] >= 0).sum(dim=1).cpu().numpy()
     rng = np.random.default_rng(11)
     tokens = sorted({0, 1, 543, *np.flatnonzero(rows <= 1)[:8].tolist(), *rng.choice(544, 24, replace=False).tolist()})
     index = torch.as_tensor(tokens, device=device)
     ref = sr.oracle_fp32(data, policy, tokens)
     assert_close(tensors["attention_out"][index].float().cpu().numpy(), ref, policy["DTYPE"])
+    lse_ref = sr.oracle_lse(data, policy, tokens)
+    assert_lse(lse[index], lse_ref)
     for parts in (None, 2, 4):
         tensors["attention_out"].fill_(float("nan"))
-        sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=parts)
+        lse.fill_(float("nan"))
+        sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=parts, softmax_lse=lse)
         torch.cuda.synchronize()
         assert guard_intact(tensors), f"kernel wrote past attention_out (parts={parts})"
         assert torch.isfinite(tensors["attention_out"].float()).all(), f"unwritten output (parts={parts})"
+        assert torch.isfinite(lse).all(), f"unwritten softmax_lse (parts={parts})"
         assert_close(tensors["attention_out"][index].float().cpu().numpy(), ref, policy["DTYPE"])
+        assert_lse(lse[index], lse_ref)
 
 
 def test_relaunch_is_bitwise_deterministic(device):
@@ -207,3 +231,46 @@ def test_prefill_from_empty_cache_has_growing_selections(device):
     inputs = make_inputs(policy, 4096, device=device)
     tokens = list(range(0, 40)) + list(range(100, 4096, 97)) + [4095]
     check_measured(inputs, tokens, device)
+
+
+def test_decode_b128x6_ctx128k_sampled_tokens(device):
+    """The reference README's second decode row (B128 x 6 queries = 768 tokens
+    at 128K, README.md:36): three full rounds of 256 work items, no split."""
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+
+    print("\n[sparse] decode B128x6 ctx 131072", flush=True)
+    policy = measurement_policy(batch=128, query_tokens=6, context=131072)
+    inputs = make_inputs(policy, 131072, device=device)
+    rng = np.random.default_rng(7)
+    tokens = sorted({0, 5, 6, 767, *rng.choice(768, 60, replace=False).tolist()})
+    check_measured(inputs, tokens, device)
+
+
+@pytest.mark.parametrize("variant", ["bf16-d512-bm64-r2", "f16-d256-bm64-r1", "bf16-d128-bm32-r2"])
+def test_framework_op_matches_entry_and_oracle(device, variant):
+    """torch.ops.ascendflow_amd.sparse_flash_mla (vendor-operator call
+    convention, sizes from shapes, output and LSE allocated) gives the same
+    bits as the drop-in entry and matches the oracle, LSE included."""
+    import ascendflow_amd.sparse_attention  # noqa: F401  registers the op
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    policy = sr.default_policy(B=4, T=16, MAX_SEQ=4096, ORI_BLOCKS=64, CMP_BLOCKS=64, **VARIANTS[variant])
+    policy["SCALE"] = policy["D"] ** -0.5
+    data = sr.inputs(policy, "mixed")
+    tensors = to_device(data, policy, device)
+    args = [tensors[k] for k in sr.TENSOR_ORDER if k != "attention_out"]
+    out, lse = torch.ops.ascendflow_amd.sparse_flash_mla(*args, policy["SCALE"], policy["RATIO"],
+                                                         ori_win_left=policy["WINDOW"] - 1, return_softmax_lse=True)
+    entry_lse = torch.empty_like(lse)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), softmax_lse=entry_lse)
+    torch.cuda.synchronize()
+    assert torch.equal(out, tensors["attention_out"]), "framework op differs from sparse_mla"
+    assert torch.equal(lse, entry_lse), "framework op softmax_lse differs from sparse_mla"
+    assert_close(out.float().cpu().numpy(), sr.oracle_fp32(data, policy), policy["DTYPE"])
+    assert_lse(lse, sr.oracle_lse(data, policy))
+    out2, empty = torch.ops.ascendflow_amd.sparse_flash_mla(*args, policy["SCALE"], policy["RATIO"],
+                                                            ori_win_left=policy["WINDOW"] - 1)
+    torch.cuda.synchronize()
+    assert empty.numel() == 0 and torch.equal(out2, out)
+    with pytest.raises(ValueError):
+        torch.ops.ascendflow_amd.sparse_flash_mla(*args, policy["SCALE"], policy["RATIO"], ori_mask_mode=1)

@@ -213,3 +213,45 @@ def test_measurement_inputs_validity_matches_oracle(ratio):
     host = make_metadata(first, 8, seed=3)
     data = dict(host, ori_kv=np.zeros((1, 128, 1, 8)), cmp_kv=np.zeros((1, 128 // ratio, 1, 8)))
     assert len(sr.selected_physical(data, first, 0)) == 1 + (ratio == 1)
+
+
+def test_lse_closed_forms_zero_query_and_empty_selection():
+    """q = 0: every score is 0, so the normaliser is ln(n + e^sink); an empty
+    selection leaves the sink alone."""
+    rng = np.random.default_rng(3)
+    rows = rng.standard_normal((7, 16)).astype(np.float32)
+    sinks = np.array([-2.0, 0.0, 1.5], np.float32)
+    q = np.zeros((3, 16), np.float32)
+    np.testing.assert_allclose(sr.attend_lse(q, rows, sinks, 0.25), np.log(7 + np.exp(sinks.astype(np.float64))),
+                               rtol=1e-15)
+    np.testing.assert_array_equal(sr.attend_lse(q, np.zeros((0, 16), np.float32), sinks, 0.25), sinks)
+
+
+def test_lse_is_logsumexp_with_the_sink_as_one_more_column():
+    from scipy.special import logsumexp
+
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((4, 32))
+    rows = rng.standard_normal((50, 32))
+    sinks = rng.standard_normal(4) * 3
+    scores = q @ rows.T * 0.3
+    expected = logsumexp(np.concatenate([scores, sinks[:, None]], axis=1), axis=1)
+    np.testing.assert_allclose(sr.attend_lse(q, rows, sinks, 0.3), expected, rtol=1e-12)
+
+
+@pytest.mark.parametrize("case", ["mixed", "sink", "empty", "duplicates"])
+def test_lse_rebuilds_the_oracle_output(case):
+    """attention_out = sum_j exp(s_j - lse) k_j: the normaliser is the
+    denominator the oracle divides by."""
+    policy = sr.default_policy(B=4, T=16, MAX_SEQ=4096, ORI_BLOCKS=64, CMP_BLOCKS=64, D=128, H=32, BM=32)
+    data = sr.inputs(policy, case)
+    out = sr.oracle_fp32(data, policy)
+    lse = sr.oracle_lse(data, policy)
+    for token in range(policy["T"]):
+        rows, _ = sr.selected_rows(data, policy, token)
+        q = np.asarray(data["q"][token], np.float64)
+        if len(rows) == 0:
+            np.testing.assert_array_equal(out[token], 0.0)
+            continue
+        weights = np.exp(q @ rows.astype(np.float64).T * policy["SCALE"] - lse[token][:, None])
+        np.testing.assert_allclose(out[token], weights @ rows, rtol=2e-4, atol=2e-6)
