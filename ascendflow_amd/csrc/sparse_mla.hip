@@ -278,6 +278,41 @@ __global__ __launch_bounds__(NTH) void sparse_plan_kernel(SparseArgs a) {
 // TAU, so P stays <= 2^TAU; the final O/l is independent of the reference point.
 constexpr float TAU = 8.0f;
 
+// Stores one 16-head tile of O, held as the PV accumulators hold it (lane
+// (i16, g) has features 16t + 4g + 0..3 of head i16, t < DPV / 16), scaled by
+// inv and rounded, through a wave-private LDS stage of 16 * DPV * 2 bytes, so
+// that each global store writes whole DPV * 2-byte head-row slices (full cache
+// lines). Stored straight from the accumulators, every instruction would write
+// 16 scattered 32-byte pieces; measured on prefill Q8K, that pattern costs ~9%
+// of the kernel. 16-byte units are XOR-swizzled by head row in the stage. The
+// stage is only touched by this wave, whose LDS operations complete in order.
+template <int DT, int DPV>
+__device__ __forceinline__ void store_head_tile(uint32_t stage, const f32x4 (&o)[DPV / 16], float inv,
+                                                typename B16<DT>::scalar* out, size_t head_stride, int lane) {
+  typedef typename B16<DT>::scalar scalar;
+  typedef typename B16<DT>::x4 x4;
+  constexpr int PVT = DPV / 16;
+  constexpr int UR = DPV / 8;       // 16-byte units per head row
+  constexpr int ROWB = DPV * 2;     // bytes per head row
+  constexpr int HPI = 1024 / ROWB;  // head rows per 1 KiB wave access
+  static_assert((UR & (UR - 1)) == 0 && 16 % HPI == 0, "power-of-two head rows of at most 1 KiB");
+  const int i16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < PVT; ++t) {
+    x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[t][k] * inv);
+    const uint32_t unit = (uint32_t)((2 * t + (g >> 1)) ^ (i16 & (UR - 1)));
+    *(AFA_LDS x4*)(uintptr_t)(stage + (uint32_t)(i16 * ROWB) + unit * 16u + (uint32_t)(g & 1) * 8u) = v;
+  }
+#pragma unroll
+  for (int r = 0; r < 16 / HPI; ++r) {
+    const int h = r * HPI + lane / UR, u = lane % UR;
+    const u32x4 w = *(const AFA_LDS u32x4*)(uintptr_t)(stage + (uint32_t)(h * ROWB) + (uint32_t)((u ^ (h & (UR - 1))) << 4));
+    *(u32x4*)((char*)(out + (size_t)h * head_stride) + u * 16) = w;
+  }
+}
+
 constexpr int NSTAGE = 3;  // KV chunk buffers in LDS
 constexpr int LOOK = 4;     // V^T fragment lookahead (16-feature tiles) of an output wave
 constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
@@ -616,19 +651,14 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     }
     __syncthreads();
     // ---- 5. normalise and store: this lane holds head head0 + 16ht + i16,
-    // features dbase + 16t + 4g + i.
+    // features dbase + 16t + 4g + i. The KV ring is idle now: each output
+    // wave stages its head tiles in its own 16 * DPV * 2 bytes of it.
+    static_assert(NP * 16 * DPV * 2 <= NSTAGE * CHUNK * ROW_BYTES, "output stage must fit the KV ring");
+    const uint32_t stage = lds_address(kv_lds[0]) + (uint32_t)((wave - NQ) * 16 * DPV * 2);
+    scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
-    for (int ht = 0; ht < NQ; ++ht) {
-      const float inv = linv_lds[16 * ht + i16];
-      scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + 16 * ht + i16) * D + dbase + 4 * g;
-#pragma unroll
-      for (int t = 0; t < PVT; ++t) {
-        x4 v;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
-        *(x4*)(out_row + 16 * t) = v;
-      }
-    }
+    for (int ht = 0; ht < NQ; ++ht)
+      store_head_tile<DT, DPV>(stage, o[ht], linv_lds[16 * ht + i16], out0 + (size_t)16 * ht * D, D, lane);
   }
 }
 
@@ -703,6 +733,10 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   __shared__ float alpha_lds[2][BMH];
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];
   __shared__ float ml_lds[2][2][BMH];  // item parity: running max (log2 units), denominator
+  // Output stage of the whole-item stores (store_head_tile), one 16-head tile
+  // per output wave; the 4-tile ring leaves no room for it (direct stores).
+  constexpr bool STAGED = NS == 3;
+  __shared__ __attribute__((aligned(16))) uint8_t out_stage[STAGED ? NP * 16 * DPV * 2 : 16];
   __shared__ __attribute__((aligned(16))) int count_lds[LISTS];
   extern __shared__ __attribute__((aligned(16))) uint32_t lists[];  // [LISTS][list_pad]
 
@@ -989,16 +1023,22 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       const int key = item_key(j), par = j & 1;
       if (item_parts(j) == 1) {
         const int token = key / head_tiles, head0 = (key % head_tiles) * a.BM;
+        scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
         for (int ht = 0; ht < NQ; ++ht) {
           const float inv = 1.0f / ml_lds[par][1][16 * ht + i16];
-          scalar* out_row = (scalar*)a.out + ((size_t)token * a.H + head0 + 16 * ht + i16) * D + dbase + 4 * g;
+          if constexpr (STAGED) {
+            store_head_tile<DT, DPV>(lds_address(out_stage) + (uint32_t)(ow * 16 * DPV * 2), o[ht], inv,
+                                     out0 + (size_t)16 * ht * D, D, lane);
+          } else {
+            scalar* out_row = out0 + (size_t)(16 * ht + i16) * D + 4 * g;
 #pragma unroll
-          for (int t = 0; t < PVT; ++t) {
-            x4 v;
+            for (int t = 0; t < PVT; ++t) {
+              x4 v;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
-            *(x4*)(out_row + 16 * t) = v;
+              for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
+              *(x4*)(out_row + 16 * t) = v;
+            }
           }
         }
         return;
