@@ -313,7 +313,6 @@ __device__ __forceinline__ void store_head_tile(uint32_t stage, const f32x4 (&o)
   }
 }
 
-constexpr int NSTAGE = 3;  // KV chunk buffers in LDS
 constexpr int LOOK = 4;     // V^T fragment lookahead (16-feature tiles) of an output wave
 constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
 
@@ -330,12 +329,13 @@ constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
 // and their LDS, VALU and MFMA phases interleave.
 //
 // Software pipeline, one barrier per step i = 0..chunks:
-//   stash KV(i) -> barrier -> fetch KV(i+1) -> score waves: QK(i), softmax(i),
-//   P(i) -> LDS slot i&1; output waves: PV(i-1) from slot (i-1)&1.
-// KV uses a ring of NSTAGE buffers: during step i the score waves read tile i
-// and the output waves tile i-1, so the stash of tile i+1 at the top of step
-// i+1 never overwrites a tile still in use.
-template <int DT, int D, int NQ, int NP>
+//   wait KV(i) -> barrier -> fetch KV(i + NS - 2) -> score waves: QK(i),
+//   softmax(i), P(i) -> LDS slot i&1; output waves: PV(i-1) from slot (i-1)&1.
+// KV uses a ring of NS tiles (3: one chunk in flight; 4: two, for streams whose
+// rows come from HBM): during step i the score waves read tile i and the output
+// waves tile i-1, so the fetch at the top of step i never overwrites a tile
+// still in use.
+template <int DT, int D, int NQ, int NP, int NS>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
@@ -353,7 +353,9 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
   static_assert(DPV % 16 == 0 && (PVT <= 8 || (DPV / 8) % 16 == 0), "output feature range");
 
-  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NSTAGE][CHUNK * ROW_BYTES];
+  constexpr int AHEAD = NS - 2;  // chunks fetched ahead of the score waves
+  static_assert(NS == 3 || NS == 4, "KV ring of 3 or 4 tiles");
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds[NS][CHUNK * ROW_BYTES];
   __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][NQ][64];  // P in B-operand layout
   __shared__ float alpha_lds[2][BMH];   // O rescale factor per head, valid when flagged
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];  // score wave q raised its running max
@@ -379,7 +381,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   // Q^T) from there once. Loading the fragments straight into registers
   // touches 64-byte pieces of 16 rows per wave load and stalls the issue of
   // every other load of the workgroup for thousands of cycles.
-  const uint32_t q_lds = lds_address(kv_lds[1]);
+  const uint32_t q_lds = lds_address(kv_lds[NS - 2]);
   constexpr int Q_LOADS = BMH * ROW_BYTES / 1024;  // 1 KiB wave loads of the Q tile
   static_assert(BMH * ROW_BYTES <= 2 * CHUNK * ROW_BYTES, "Q tile must fit ring tiles 1 and 2");
   auto copy_q = [&]() {
@@ -437,7 +439,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   const char* cmp = (const char*)a.cmp_kv;
   const uint32_t kv_base = lds_address(kv_lds[0]);
   auto tile_address = [&](int chunk) {
-    return opaque_uniform(kv_base + (uint32_t)(chunk % NSTAGE) * (CHUNK * ROW_BYTES));
+    return opaque_uniform(kv_base + (uint32_t)(chunk % NS) * (CHUNK * ROW_BYTES));
   };
   uint32_t unit_offset[PIECES];  // ROW_LOADS: byte offset of the unit this lane loads
 #pragma unroll
@@ -473,19 +475,26 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       }
     }
   };
-  // Pipeline step i: wait for KV(i), barrier, fetch KV(i+1), then the role's work.
+  // Pipeline step i: wait for KV(i), barrier, fetch KV(i + AHEAD), then the
+  // role's work. Loads complete in issue order, so KV(i) has landed once at
+  // most the younger batch (KV(i + 1), with a 4-tile ring) is in flight.
   if (chunks > 0) {
     if constexpr (ROW_LOADS) read_entries(0);
     fetch(0);
-    // Q has landed once at most the PIECES loads of fetch(0) are in flight.
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+    if (AHEAD > 1 && chunks > 1) {
+      fetch(1);
+      // Q has landed once at most the loads of the two prologue fetches are in flight.
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * PIECES) & 15) | (((2 * PIECES) >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+    }
   } else {
     __builtin_amdgcn_s_waitcnt(0x0F70);
   }
   block_barrier();
   // Score wave fragments: this lane holds head 16 * wave + i16 (tile row r),
   // features 32j + 8g .. +7, i.e. unit 4j + g of row r, stored at unit
-  // (4j + g) ^ (r & 15). Tile 1 is overwritten only after the next barrier.
+  // (4j + g) ^ (r & 15). Its ring tiles are overwritten only after the next barrier.
   const int qhead = head0 + 16 * wave + i16;   // score wave: this lane's head
   x8 qf[QK_STEPS];
   if (scorer) {
@@ -495,9 +504,14 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       qf[j] = *lds_at<x8>(q_lds + (uint32_t)(r * ROW_BYTES + (((4 * j + g) ^ (r & 15)) << 4)));
   }
   auto step_begin = [&](int i) {
-    if (i < chunks) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (i < chunks) {
+      if (AHEAD > 1 && i + 1 < chunks)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+      else
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     block_barrier();
-    if (i + 1 < chunks) fetch(i + 1);
+    if (i + AHEAD < chunks) fetch(i + AHEAD);
   };
 
   // The swizzle only permutes units within aligned groups of 16 (256 bytes),
@@ -653,7 +667,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     // ---- 5. normalise and store: this lane holds head head0 + 16ht + i16,
     // features dbase + 16t + 4g + i. The KV ring is idle now: each output
     // wave stages its head tiles in its own 16 * DPV * 2 bytes of it.
-    static_assert(NP * 16 * DPV * 2 <= NSTAGE * CHUNK * ROW_BYTES, "output stage must fit the KV ring");
+    static_assert(NP * 16 * DPV * 2 <= NS * CHUNK * ROW_BYTES, "output stage must fit the KV ring");
     const uint32_t stage = lds_address(kv_lds[0]) + (uint32_t)((wave - NQ) * 16 * DPV * 2);
     scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
@@ -1413,10 +1427,16 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
       }
     }
   }
-  const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP>, lds);
-  if (fit) return fit;
+  // One workgroup per item: a 4-tile ring (two chunks in flight) where it
+  // fits, since the kernel runs short streams whose rows mostly come from HBM.
   const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
-  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
+  if (fits_lds(sparse_mla_kernel<DT, D, NQ, NP, 4>, lds) == AFA_OK) {
+    hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 4>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
+    return (int)hipGetLastError();
+  }
+  const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP, 3>, lds);
+  if (fit) return fit;
+  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 3>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   return (int)hipGetLastError();
 }
 
