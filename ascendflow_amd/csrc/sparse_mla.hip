@@ -154,11 +154,12 @@ __device__ __forceinline__ const T* row_pointer(const SparseArgs& a, uint32_t en
 // Resolves the selected rows of `token` into row_list (LDS) in slot order
 // (window positions, then compressed ranks) and returns their count. Every
 // one of the NTH threads of the workgroup must call it (workgroup barriers);
-// wave_count is LDS scratch of [3][NTH / 64], request_scratch of [NTH / 64].
+// wave_count is LDS scratch of [GP][NTH / 64], request_scratch of [NTH / 64].
 // Three dependent global round trips: the request count with the compressed
 // indices, then the geometry with the compressed page lookups, then the window
-// page lookups (gather.py:8-60, 116-127; attention.py:339-341).
-template <int NTH>
+// page lookups (gather.py:8-60, 116-127; attention.py:339-341); GP passes of
+// NTH slots go together, so WINDOW + TOPK <= GP * NTH takes one such sequence.
+template <int NTH, int GP>
 __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint32_t* row_list,
                                             int (*wave_count)[NTH / 64], int* request_scratch,
                                             Geometry& geo) {
@@ -170,7 +171,6 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
   // have cu[b] == cu[b+1] and are skipped).
   int below = 0;
   for (int b = tid; b < a.B; b += NTH) below += a.cu[b] <= token ? 1 : 0;
-  constexpr int GP = 2;  // passes of NTH slots resolved together
   int index[GP];
   auto load_indices = [&](int s0) {
 #pragma unroll
@@ -260,11 +260,13 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
 template <int NTH>
 __global__ __launch_bounds__(NTH) void sparse_plan_kernel(SparseArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t plan_list[];
-  __shared__ int wave_count[3][NTH / 64];
+  // Three passes of 256 slots: WINDOW + TOPK = 640 in one round-trip sequence.
+  constexpr int GP = 3;
+  __shared__ int wave_count[GP][NTH / 64];
   __shared__ int request_scratch[NTH / 64];
   const int token = blockIdx.x;
   Geometry geo;
-  const int n = resolve_rows<NTH>(a, token, plan_list, wave_count, request_scratch, geo);
+  const int n = resolve_rows<NTH, GP>(a, token, plan_list, wave_count, request_scratch, geo);
   // An empty list becomes one chunk of row 0 of ori_kv (every score masked),
   // so every token has at least one chunk to stream.
   const int padded = n > 0 ? (n + CHUNK - 1) / CHUNK * CHUNK : CHUNK;
@@ -360,7 +362,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   __shared__ float alpha_lds[2][BMH];   // O rescale factor per head, valid when flagged
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];  // score wave q raised its running max
   __shared__ float linv_lds[BMH];       // 1 / softmax denominator per head
-  __shared__ int wave_count[3][NW];
+  __shared__ int wave_count[2][NW];
   extern __shared__ __attribute__((aligned(16))) uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
   const int tid = threadIdx.x;
@@ -403,7 +405,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   int n_rows;
   {
     Geometry geo;
-    n_rows = resolve_rows<NT>(a, token, row_list, wave_count, request_scratch, geo);
+    n_rows = resolve_rows<NT, 2>(a, token, row_list, wave_count, request_scratch, geo);
     // Pad the last chunk with a real row so every load is unconditional; the
     // padded rows get -inf scores (P = 0) below.
     const int padded = (n_rows + CHUNK - 1) / CHUNK * CHUNK;
