@@ -404,6 +404,9 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   __shared__ int request_scratch[NW];
   int n_rows;
   {
+    // Q does not depend on the row list: its copy goes out first and lands
+    // while the rows are resolved (three dependent round trips).
+    copy_q();
     Geometry geo;
     n_rows = resolve_rows<NT, 2>(a, token, row_list, wave_count, request_scratch, geo);
     // Pad the last chunk with a real row so every load is unconditional; the
@@ -420,7 +423,6 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
         ((int2*)a.debug_rows)[(size_t)token * a.S + s] = r;
       }
     }
-    copy_q();
     block_barrier();
   }
   const int chunks = (n_rows + CHUNK - 1) / CHUNK;
