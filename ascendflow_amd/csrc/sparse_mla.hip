@@ -67,7 +67,7 @@ struct SparseArgs {
   int32_t* debug_rows;
   uint32_t* plan_rows;   // workspace: [T][list_pad] padded row lists, or null
   int32_t* plan_count;   // workspace: [T] selected rows per token
-  float* partials;       // workspace: [split tiles][parts][output waves][record] of split work items
+  void* partials;        // workspace: [split keys][parts][output waves] records (store_record)
   int32_t B, T, H, D, PAGE, RATIO, table_width, ori_blocks, cmp_blocks, WINDOW, TOPK, S, BM;
   int32_t list_pad;      // row-list capacity: WINDOW + TOPK rounded up to 256 (whole KiB)
   int32_t parts;         // parts each split (token, head tile) is divided into (persistent kernel)
@@ -255,6 +255,20 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
   return n_rows;
 }
 
+// A token's chunk list split into P parts: part p covers list chunks
+// [p * n / P, (p + 1) * n / P) of the token's n = max(1, ceil(count / CHUNK))
+// chunks. An empty part (n < P) streams one fully masked chunk (list chunk 0),
+// so every work item has at least one chunk and one partial result.
+struct PartRange {
+  int first;  // first list chunk of the part
+  int n;      // list chunks of the part; 0 for the masked placeholder
+};
+__device__ __forceinline__ PartRange part_range(int count, int part, int parts) {
+  const int nch = max(1, (count + CHUNK - 1) / CHUNK);
+  const int c0 = part * nch / parts, c1 = (part + 1) * nch / parts;
+  return PartRange{c0, c1 - c0};
+}
+
 // Plan kernel: one workgroup per token writes the token's row list, padded
 // with its first row to a whole number of CHUNK-row chunks, and the count.
 template <int NTH>
@@ -273,6 +287,40 @@ __global__ __launch_bounds__(NTH) void sparse_plan_kernel(SparseArgs a) {
   uint32_t* dst = a.plan_rows + (size_t)token * a.list_pad;
   for (int r = threadIdx.x; r < padded; r += NTH) dst[r] = n > 0 ? plan_list[r < n ? r : 0] : 0u;
   if (threadIdx.x == 0) a.plan_count[token] = n;
+}
+
+// Partial result of one part of a split key, for sparse_merge_kernel: output
+// wave ow's record holds its O slice normalised by the part's own denominator
+// and rounded to the storage dtype, as x4 at (ht * PVT + t) * 64 + lane (head
+// 16 ht + (lane & 15), features ow * DPV + 16 t + 4 (lane >> 4) + 0..3), then
+// the part's running max (log2 units) and denominator of the BMH heads.
+template <int DT> __host__ __device__ constexpr size_t record_bytes(int bmh, int dpv) {
+  return (size_t)bmh * dpv * sizeof(typename B16<DT>::scalar) + 2 * (size_t)bmh * sizeof(float);
+}
+template <int DT, int NQ, int NP, int DPV>
+__device__ __forceinline__ void store_record(const SparseArgs& a, int split_key, int part, int ow,
+                                             const f32x4 (&o)[NQ][DPV / 16], const float* linv,
+                                             const float (*ml)[16 * NQ], int lane) {
+  typedef typename B16<DT>::scalar scalar;
+  typedef typename B16<DT>::x4 x4;
+  constexpr int BMH = 16 * NQ, PVT = DPV / 16;
+  char* rec = (char*)a.partials + (((size_t)split_key * a.parts + part) * NP + ow) * record_bytes<DT>(BMH, DPV);
+#pragma unroll
+  for (int ht = 0; ht < NQ; ++ht) {
+    const float inv = linv[16 * ht + (lane & 15)];
+#pragma unroll
+    for (int t = 0; t < PVT; ++t) {
+      x4 v;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
+      *(x4*)(rec + (size_t)((ht * PVT + t) * 64 + lane) * sizeof(x4)) = v;
+    }
+  }
+  float* stats = (float*)(rec + (size_t)BMH * DPV * sizeof(scalar));
+  if (lane < BMH) {
+    stats[lane] = ml[0][lane];
+    stats[BMH + lane] = ml[1][lane];
+  }
 }
 
 // Lazy rescaling threshold (log2 units): the running max used for exp2 is only
@@ -362,6 +410,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   __shared__ float alpha_lds[2][BMH];   // O rescale factor per head, valid when flagged
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];  // score wave q raised its running max
   __shared__ float linv_lds[BMH];       // 1 / softmax denominator per head
+  __shared__ float ml_lds[2][BMH];      // running max (log2 units) and denominator per head
   __shared__ int wave_count[2][NW];
   extern __shared__ __attribute__((aligned(16))) uint32_t row_list[];  // round_up(WINDOW + TOPK, CHUNK) entries
 
@@ -372,9 +421,24 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   const int g = lane >> 4, i16 = lane & 15;
   const bool scorer = wave < NQ;
   const int head_tiles = a.H / a.BM;
-  const uint32_t logical = xcd_contiguous(blockIdx.x, gridDim.x);
-  const int token = (int)(logical / head_tiles);
-  const int head0 = (int)(logical % head_tiles) * a.BM;
+  // Whole keys and split parts are each spread XCD-contiguously on their own
+  // (when split_from is a multiple of the 8 XCDs, the hardware block ids of the
+  // two segments then fall on the same XCD pattern): over the whole grid, the
+  // XCDs holding the low logical ids would get every whole key and the others
+  // only parts.
+  const uint32_t s0 = (uint32_t)a.split_from;  // <= gridDim.x
+  const int logical = (int)((s0 & 7u) != 0 ? xcd_contiguous(blockIdx.x, gridDim.x)
+                            : blockIdx.x < s0 ? xcd_contiguous(blockIdx.x, s0)
+                                              : s0 + xcd_contiguous(blockIdx.x - s0, gridDim.x - s0));
+  // Work item: key (token, head tile) `logical` below split_from, whole; from
+  // split_from on, item split_from + k * parts + p is part p of key
+  // split_from + k (a contiguous range of its list chunks, merged afterwards).
+  const int S0 = a.split_from, P = a.parts;
+  const bool split = logical >= S0;
+  const int key = split ? S0 + (logical - S0) / P : logical;
+  const int part = split ? (logical - S0) % P : 0;
+  const int token = key / head_tiles;
+  const int head0 = (key % head_tiles) * a.BM;
 
   // ---- 1-2. the token's row list in LDS and Q. Q (BMH contiguous rows of D features) is copied with the
   // load-to-LDS path in coalesced 1 KiB wave loads into ring tiles 1 and 2,
@@ -413,6 +477,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     // padded rows get -inf scores (P = 0) below.
     const int padded = (n_rows + CHUNK - 1) / CHUNK * CHUNK;
     if (tid < padded - n_rows) row_list[n_rows + tid] = row_list[0];
+    // A part of an empty selection streams one masked chunk of ori row 0.
+    if (split && n_rows == 0 && tid < CHUNK) row_list[tid] = 0u;
     if (a.debug_rows != nullptr && head0 == 0) {
       const int slots = a.WINDOW + geo.count_cmp;
       for (int s = tid; s < a.S; s += NT) {
@@ -425,7 +491,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     }
     block_barrier();
   }
-  const int chunks = (n_rows + CHUNK - 1) / CHUNK;
+  // This item's list chunks: all of them, or its part's range (an empty part
+  // streams one fully masked chunk of list chunk 0).
+  const PartRange range = split ? part_range(n_rows, part, P) : PartRange{0, (n_rows + CHUNK - 1) / CHUNK};
+  const bool placeholder = split && range.n == 0;
+  const int chunks = placeholder ? 1 : range.n;
+  auto list_chunk = [&](int i) { return placeholder ? 0 : range.first + i; };
 
   // ---- 3. KV movement: global -> LDS through the load-to-LDS path ------------
   // global_load_lds_dwordx4 writes one wave's 64 x 16 bytes contiguously at the
@@ -451,7 +522,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   uint32_t entry_next[PIECES];
   auto read_entries = [&](int chunk) {
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) entry_next[p] = row_list[chunk * CHUNK + wave * PIECES + p];
+    for (int p = 0; p < PIECES; ++p) entry_next[p] = row_list[list_chunk(chunk) * CHUNK + wave * PIECES + p];
   };
   auto fetch = [&](int chunk) {
     const uint32_t tile = tile_address(chunk);
@@ -471,7 +542,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       for (int p = 0; p < PIECES; ++p) {
         const int flat = tid + p * NT;
         const int r = flat / UNITS, upos = flat % UNITS;
-        const uint32_t e = row_list[chunk * CHUNK + r];
+        const uint32_t e = row_list[list_chunk(chunk) * CHUNK + r];
         const char* src = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES + ((upos ^ (r & 15)) << 4);
         const uint32_t dst = tile + (uint32_t)((wave * 64 + p * NT) * 16);
         __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
@@ -527,7 +598,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     // exceeds it by more than TAU. This lane holds S^T rows sigma(4g+i) and
     // 16 + sigma(4g+i) of head qhead.
     float m_run = a.sinks[qhead] * LOG2E;
-    float l_run = g == 0 ? 1.0f : 0.0f;  // e^(sink - m) counted once per head
+    float l_run = (g == 0 && part == 0) ? 1.0f : 0.0f;  // e^(sink - m), once per head and token
     const float scale_log2 = a.scale * LOG2E;
     const int ra = sigma(i16);           // KV fragment row inside a 16-row tile
     uint32_t qk_base[4];
@@ -568,7 +639,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       const int slot = i & 1;
       float x0[4], x1[4];
       float cmax = -INFINITY;
-      const int live = n_rows - i * CHUNK;
+      const int live = placeholder ? 0 : n_rows - list_chunk(i) * CHUNK;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         x0[k] = s0[k];
@@ -606,8 +677,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     }
     const float l = sum_over_lane_groups(l_run);
     if (g == 0) {
-      linv_lds[16 * wave + i16] = 1.0f / l;
-      if (a.lse != nullptr) a.lse[(size_t)token * a.H + qhead] = lse_of(m_run, l);
+      // l = 0 only for a split part without rows (its O is 0 and its merge
+      // weight l 2^(m - M) is 0); without the sink it has no denominator.
+      linv_lds[16 * wave + i16] = l > 0.f ? 1.0f / l : 0.f;
+      ml_lds[0][16 * wave + i16] = m_run;
+      ml_lds[1][16 * wave + i16] = l;
+      if (a.lse != nullptr && !split) a.lse[(size_t)token * a.H + qhead] = lse_of(m_run, l);
     }
     __syncthreads();
   } else {
@@ -672,26 +747,16 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     // features dbase + 16t + 4g + i. The KV ring is idle now: each output
     // wave stages its head tiles in its own 16 * DPV * 2 bytes of it.
     static_assert(NP * 16 * DPV * 2 <= NS * CHUNK * ROW_BYTES, "output stage must fit the KV ring");
+    if (split) {
+      store_record<DT, NQ, NP, DPV>(a, key - S0, part, wave - NQ, o, linv_lds, ml_lds, lane);
+      return;
+    }
     const uint32_t stage = lds_address(kv_lds[0]) + (uint32_t)((wave - NQ) * 16 * DPV * 2);
     scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
     for (int ht = 0; ht < NQ; ++ht)
       store_head_tile<DT, DPV>(stage, o[ht], linv_lds[16 * ht + i16], out0 + (size_t)16 * ht * D, D, lane);
   }
-}
-
-// A token's chunk list split into P parts: part p covers list chunks
-// [p * n / P, (p + 1) * n / P) of the token's n = max(1, ceil(count / CHUNK))
-// chunks. An empty part (n < P) streams one fully masked chunk (list chunk 0),
-// so every work item has at least one chunk and one partial result.
-struct PartRange {
-  int first;  // first list chunk of the part
-  int n;      // list chunks of the part; 0 for the masked placeholder
-};
-__device__ __forceinline__ PartRange part_range(int count, int part, int parts) {
-  const int nch = max(1, (count + CHUNK - 1) / CHUNK);
-  const int c0 = part * nch / parts, c1 = (part + 1) * nch / parts;
-  return PartRange{c0, c1 - c0};
 }
 
 // Stream position: chunk c of work item j (workgroup-local index), whose part
@@ -703,13 +768,9 @@ struct Cursor {
 };
 
 // Persistent form for the plan workspace: one workgroup per CU walks its work
-// items worker, worker + G, ... (G workgroups) as ONE continuous chunk stream,
-// so an item boundary costs no pipeline drain and no dependent global round
-// trip. Work items are the (token, BM-head tile) keys below split_from, whole,
-// then P parts of each key from split_from on: a split key's chunk list is
-// divided over P workgroups (so the last round of a short stream, such as
-// decode, keeps every CU busy to the end) and each part stores its
-// unnormalised (m, l, O) record for sparse_merge_kernel, which runs next.
+// items worker, worker + G, ... (G workgroups; an item is one (token, BM-head
+// tile) key) as ONE continuous chunk stream, so an item boundary costs no
+// pipeline drain and no dependent global round trip.
 //  - the KV ring of NS tiles, P slots and step parities run on across items;
 //    output waves fetch KV rows AHEAD = NS - 2 chunks ahead of the score waves
 //    (two chunks in flight hide the HBM latency of short streams);
@@ -739,7 +800,6 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   constexpr int PIECES = CHUNK * UNITS / NO;   // 16-byte loads per output thread per chunk
   constexpr int AHEAD = NS - 2;                // chunks fetched ahead of the score waves
   constexpr int LISTS = AHEAD + 3;             // row-list ring (items j - 1 .. j + AHEAD + 1 in use)
-  constexpr int REC = BMH * DPV + 2 * BMH;     // floats of one output wave's partial record
   static_assert(NS == 3 || NS == 4, "KV ring of 3 or 4 tiles");
   static_assert(CHUNK * UNITS % NO == 0, "chunk must split evenly over the output waves");
   static_assert(UNITS >= 16, "swizzle needs at least 16 units per row");
@@ -763,27 +823,17 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   const int g = lane >> 4, i16 = lane & 15;
   const bool scorer = wave < NQ;
   const int head_tiles = a.H / a.BM;
-  const int P = a.parts, S0 = a.split_from;
-  const int n_items = S0 + (a.T * head_tiles - S0) * P;
+  const int n_items = a.T * head_tiles;
   const int G = (int)gridDim.x;
   const int worker = (int)xcd_contiguous(blockIdx.x, gridDim.x);
   const int J = (n_items - worker + G - 1) / G;  // items of this workgroup (>= 1: G <= n_items)
-  // Item i < S0 is key i, whole; item S0 + k * P + p is part p of key S0 + k.
-  auto item_key = [&](int j) {
-    const int i = worker + j * G;
-    return i < S0 ? i : S0 + (i - S0) / P;
-  };
-  auto item_part = [&](int j) {
-    const int i = worker + j * G;
-    return i < S0 ? 0 : (i - S0) % P;
-  };
-  auto item_parts = [&](int j) { return worker + j * G < S0 ? 1 : P; };
+  auto item_key = [&](int j) { return worker + j * G; };
   auto item_token = [&](int j) { return item_key(j) / head_tiles; };
   auto item_head0 = [&](int j) { return (item_key(j) % head_tiles) * a.BM; };
   const uint32_t list_base = lds_address(lists);
   auto list_address = [&](int j) { return list_base + (uint32_t)((j % LISTS) * a.list_pad) * 4u; };
   auto start = [&](Cursor& k, int j) {
-    const PartRange r = part_range(count_lds[j % LISTS], item_part(j), item_parts(j));
+    const PartRange r = part_range(count_lds[j % LISTS], 0, 1);
     k.j = j;
     k.c = 0;
     k.first = r.first;
@@ -941,7 +991,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
           sink = sink_next;
         }
         m_run = sink;
-        l_run = (g == 0 && item_part(cur.j) == 0) ? 1.0f : 0.0f;  // e^(sink - m), once per head
+        l_run = g == 0 ? 1.0f : 0.0f;  // e^(sink - m) counted once per head
         if (cur.j + 1 < J) {
           const int head = item_head0(cur.j + 1) + 16 * wave + i16;
           const scalar* q_row = (const scalar*)a.q + ((size_t)item_token(cur.j + 1) * a.H + head) * D + 8 * g;
@@ -1017,7 +1067,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
         if (g == 0) {
           ml_lds[cur.j & 1][0][16 * wave + i16] = m_run;
           ml_lds[cur.j & 1][1][16 * wave + i16] = l;
-          if (a.lse != nullptr && item_parts(cur.j) == 1)
+          if (a.lse != nullptr)
             a.lse[(size_t)item_token(cur.j) * a.H + item_head0(cur.j) + 16 * wave + i16] = lse_of(m_run, l);
         }
       }
@@ -1035,40 +1085,27 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       tr_base[b] = (uint32_t)(rt * ROW_BYTES + (((dbase / 8 + 2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
 
     // Output of item j: this lane holds heads head0 + 16ht + i16, features
-    // dbase + 16t + 4g + i. A whole item stores O / l; a part stores its
-    // record (O as f32x4 at (ht * PVT + t) * 64 + lane, then m[BMH], l[BMH]).
+    // dbase + 16t + 4g + i.
     auto finish = [&](int j) {
       const int key = item_key(j), par = j & 1;
-      if (item_parts(j) == 1) {
-        const int token = key / head_tiles, head0 = (key % head_tiles) * a.BM;
-        scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
+      const int token = key / head_tiles, head0 = (key % head_tiles) * a.BM;
+      scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
-        for (int ht = 0; ht < NQ; ++ht) {
-          const float inv = 1.0f / ml_lds[par][1][16 * ht + i16];
-          if constexpr (STAGED) {
-            store_head_tile<DT, DPV>(lds_address(out_stage) + (uint32_t)(ow * 16 * DPV * 2), o[ht], inv,
-                                     out0 + (size_t)16 * ht * D, D, lane);
-          } else {
-            scalar* out_row = out0 + (size_t)(16 * ht + i16) * D + 4 * g;
+      for (int ht = 0; ht < NQ; ++ht) {
+        const float inv = 1.0f / ml_lds[par][1][16 * ht + i16];
+        if constexpr (STAGED) {
+          store_head_tile<DT, DPV>(lds_address(out_stage) + (uint32_t)(ow * 16 * DPV * 2), o[ht], inv,
+                                   out0 + (size_t)16 * ht * D, D, lane);
+        } else {
+          scalar* out_row = out0 + (size_t)(16 * ht + i16) * D + 4 * g;
 #pragma unroll
-            for (int t = 0; t < PVT; ++t) {
-              x4 v;
+          for (int t = 0; t < PVT; ++t) {
+            x4 v;
 #pragma unroll
-              for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
-              *(x4*)(out_row + 16 * t) = v;
-            }
+            for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
+            *(x4*)(out_row + 16 * t) = v;
           }
         }
-        return;
-      }
-      float* rec = a.partials + (((size_t)(key - S0) * P + item_part(j)) * NP + ow) * REC;
-#pragma unroll
-      for (int ht = 0; ht < NQ; ++ht)
-#pragma unroll
-        for (int t = 0; t < PVT; ++t) *(f32x4*)(rec + ((ht * PVT + t) * 64 + lane) * 4) = o[ht][t];
-      if (lane < BMH) {
-        rec[BMH * DPV + lane] = ml_lds[par][0][lane];
-        rec[BMH * DPV + BMH + lane] = ml_lds[par][1][lane];
       }
     };
 
@@ -1152,15 +1189,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   }
 }
 
-// Merge of split work items. A record (one per split key, part and output
-// wave ow) holds that wave's O slice as f32x4 at (ht * PVT + t) * 64 + lane
-// (head 16 ht + (lane & 15), features ow * D/NP + 16 t + 4 (lane >> 4) + 0..3),
-// then the running max (log2 units) and denominator of its BM heads. One
-// workgroup per (split key, ow, ht) slice of 16 heads, each thread issuing all
-// of its parts' loads at once, combines the parts in part order
-// (deterministic):
-//   M = max_p m_p, w_p = 2^(m_p - M), O = (sum_p w_p O_p) / (sum_p w_p l_p),
-// the online-softmax merge of attention.py:398-525's running max/denominator
+// Merge of split work items (records: store_record). One workgroup per
+// (split key, output wave ow, 16-head tile) slice, each thread issuing all of
+// its parts' loads at once, combines the parts in part order (deterministic):
+// with M = max_p m_p and w_p = 2^(m_p - M) l_p (part p's denominator relative
+// to M), O = sum_p w_p O_p / sum_p w_p, O_p the part's normalised output: the
+// online-softmax merge of attention.py:398-525's running max and denominator
 // over disjoint row sets (the sink's term is in part 0's denominator).
 template <int D, int NP>
 constexpr int merge_threads() {  // threads per 16-head slice: at most 256
@@ -1173,32 +1207,32 @@ __global__ __launch_bounds__((merge_threads<D, NP>())) void sparse_merge_kernel(
   constexpr int BMH = 16 * NQ;
   constexpr int DPV = D / NP;
   constexpr int PVT = DPV / 16;
-  constexpr int REC = BMH * DPV + 2 * BMH;
   constexpr int MT = merge_threads<D, NP>();
-  constexpr int PER = PVT * 64 / MT;  // f32x4 of a 16-head slice per thread
+  constexpr int PER = PVT * 64 / MT;  // x4 of a 16-head slice per thread
   static_assert(PVT * 64 % MT == 0 && PER >= 1 && PER <= 4, "slice must split evenly over the threads");
+  constexpr size_t REC = record_bytes<DT>(BMH, DPV);
   const int slice = (int)blockIdx.x % (NP * NQ), split_key = (int)blockIdx.x / (NP * NQ);
   const int ow = slice / NQ, ht = slice % NQ;
   const int head_tiles = a.H / a.BM;
   const int key = a.split_from + split_key;
   const int token = key / head_tiles, head0 = (key % head_tiles) * a.BM;
   const int P = a.parts;
-  const size_t part_stride = (size_t)NP * REC;
-  const float* records = a.partials + ((size_t)split_key * P * NP + ow) * REC;
-  // Thread tid holds f32x4 number ht * PVT * 64 + k * MT + tid of the O
-  // slice: tile t = (k * MT + tid) / 64, lane = tid % 64.
+  // Thread tid holds x4 number ht * PVT * 64 + k * MT + tid of the slice:
+  // tile t = (k * MT + tid) / 64, lane = tid % 64.
   const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
   const int h = 16 * ht + i16;
   float mq[MAX_PARTS], lq[MAX_PARTS];
-  f32x4 oq[MAX_PARTS][PER];
+  x4 oq[MAX_PARTS][PER];
 #pragma unroll
   for (int q = 0; q < MAX_PARTS; ++q) {
     if (q < P) {
-      const float* rec = records + q * part_stride;
-      mq[q] = rec[BMH * DPV + h];
-      lq[q] = rec[BMH * DPV + BMH + h];
+      const char* rec = (const char*)a.partials + (((size_t)split_key * P + q) * NP + ow) * REC;
+      const float* stats = (const float*)(rec + (size_t)BMH * DPV * sizeof(scalar));
+      mq[q] = stats[h];
+      lq[q] = stats[BMH + h];
 #pragma unroll
-      for (int k = 0; k < PER; ++k) oq[q][k] = *(const f32x4*)(rec + (ht * PVT * 64 + k * MT + threadIdx.x) * 4);
+      for (int k = 0; k < PER; ++k)
+        oq[q][k] = *(const x4*)(rec + (size_t)(ht * PVT * 64 + k * MT + threadIdx.x) * sizeof(x4));
     }
   }
   float M = -INFINITY;
@@ -1212,10 +1246,12 @@ __global__ __launch_bounds__((merge_threads<D, NP>())) void sparse_merge_kernel(
 #pragma unroll
   for (int q = 0; q < MAX_PARTS; ++q) {
     if (q < P) {
-      const float w = fast_exp2(mq[q] - M);
-      L += lq[q] * w;
+      const float w = fast_exp2(mq[q] - M) * lq[q];
+      L += w;
 #pragma unroll
-      for (int k = 0; k < PER; ++k) acc[k] += oq[q][k] * w;
+      for (int k = 0; k < PER; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[k][e] += (float)oq[q][k][e] * w;
     }
   }
   const float inv = 1.0f / L;
@@ -1276,36 +1312,56 @@ static int check_sparse(const SparseMlaParams* p) {
   return AFA_OK;
 }
 
-// Split of the (token, BM-head tile) keys for the persistent kernel. With R
-// full rounds of 256 keys (a fixed model of MI355X's 256 compute units keeps
-// the workspace size a function of the sizes alone) and r keys left over, the
-// last round would keep only r CUs busy for a whole key's chunks. Splitting
-// those r keys into P = min(MAX_PARTS, 256 / r) parts gives every CU at most
-// one part in that round. The plan kernel, the parts' FP32 records and the
-// merge kernel cost about MERGE_COST chunk steps (measured on decode B64 x 6:
-// plan 6.7 us + merge 8.5 us, ~1.5 us per chunk step), so a split is taken only
-// where it shortens the longest stream by more: small batches (T = 16: 3 chunk
-// steps + merge instead of 20), not decode B64 x 6 (20 + 10 + merge against
-// 40). parts = 1 never splits; parts > 1 splits every key into that many parts.
+// Split of the (token, BM-head tile) keys of short streams (at most one full
+// round of 256 keys; a fixed model of MI355X's 256 compute units keeps the
+// workspace size a function of the sizes alone). With r keys beyond the full
+// rounds, the last round keeps only r CUs busy for a whole key's chunks;
+// splitting those keys into P parts (r P <= 256) shortens that round, and the
+// merge kernel then combines the parts' records. Costs are in chunk steps of a
+// fully loaded GPU (256 CUs streaming 32-row chunks, HBM-bound: ~1.4 us at
+// D = 512, measured with per-workgroup real-time stamps on decode): a round of
+// n streams of c chunks costs SPLIT_SETUP (row resolution and Q) plus
+// c * max(SPLIT_LATENCY, n / 256) (fewer streams run latency-bound, not
+// faster); the merge costs its launch gap plus its traffic (records written and
+// read back, output written) at the loaded rate of 256 chunks per step. The
+// cheapest P is taken if it beats the whole last round: decode B1..B16 x 6 and
+// B48 x 6 split; B64 x 6 (128 keys beyond one round: 10 loaded steps plus a
+// merge of 7 against 20 latency-bound ones of 0.7) does not, nor does anything
+// with two or more full rounds (those run on the persistent kernel).
+// parts = 1 never splits; parts > 1 splits every key into that many parts.
 struct Split {
   int parts;           // parts of each split key (1: nothing split)
   int64_t split_from;  // first split key
 };
 constexpr int64_t SPLIT_MODEL_CUS = 256;
-constexpr int64_t MERGE_COST = 10;
+constexpr double SPLIT_SETUP = 3.5, SPLIT_LATENCY = 0.7, MERGE_GAP = 2.0;
+static int64_t record_bytes_per_part(const SparseMlaParams* p) {
+  // BM heads x D features of the storage dtype, plus FP32 (max, denominator)
+  // per head and output wave (BM / 16 output waves).
+  return 2LL * p->BM * p->D + (int64_t)p->BM * p->BM / 2;
+}
 static Split choose_split(const SparseMlaParams* p) {
   const int64_t tiles = (int64_t)p->T * (p->H / p->BM);
   if (p->parts == 1) return Split{1, tiles};
   if (p->parts > 1) return Split{p->parts, 0};
   const int64_t nch = std::max<int64_t>(1, (p->WINDOW + p->TOPK + CHUNK - 1) / CHUNK);
   const int64_t rounds = tiles / SPLIT_MODEL_CUS, rest = tiles % SPLIT_MODEL_CUS;
-  if (rest == 0) return Split{1, tiles};
-  const int parts = (int)std::min<int64_t>(std::min<int64_t>(MAX_PARTS, SPLIT_MODEL_CUS / rest), nch);
-  if (parts < 2) return Split{1, tiles};
-  const int64_t whole = (rounds + 1) * nch;
-  const int64_t split = rounds * nch + (nch + parts - 1) / parts + MERGE_COST;
-  if (split >= whole) return Split{1, tiles};
-  return Split{parts, rounds * SPLIT_MODEL_CUS};
+  if (rest == 0 || rounds > 1) return Split{1, tiles};
+  const double cus = (double)SPLIT_MODEL_CUS;
+  auto round_cost = [&](int64_t n, int64_t c) { return SPLIT_SETUP + c * std::max(SPLIT_LATENCY, n / cus); };
+  const double step_bytes = cus * CHUNK * p->D * 2.0;
+  Split best{1, tiles};
+  double best_cost = round_cost(rest, nch);
+  const int64_t max_parts = std::min<int64_t>(std::min<int64_t>(MAX_PARTS, SPLIT_MODEL_CUS / rest), nch);
+  for (int64_t parts = 2; parts <= max_parts; ++parts) {
+    const double traffic = (double)rest * (2.0 * parts * record_bytes_per_part(p) + 2.0 * p->BM * p->D);
+    const double cost = round_cost(rest * parts, (nch + parts - 1) / parts) + MERGE_GAP + traffic / step_bytes;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = Split{(int)parts, rounds * SPLIT_MODEL_CUS};
+    }
+  }
+  return best;
 }
 
 static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void* ori_kv,
@@ -1356,8 +1412,9 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
 // Plan workspace, each slice starting on a 256-byte boundary:
 //   [T] counts | [T][list_pad] row lists | partial records of split keys,
 //   [split keys][parts][BM / 16 output waves][BM * D / (BM / 16) + 2 * BM]
-//   floats: per (key, part) BM * D + BM * BM / 8 floats (each output wave's
-//   O slice, and the running max and denominator of every head).
+//   bytes: per (key, part) 2 * BM * D + BM * BM / 2 (each output wave's
+//   normalised O slice in the storage dtype, and the running max and
+//   denominator of every head, store_record).
 static size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 static size_t plan_count_bytes(int64_t T) { return round256((size_t)T * 4); }
 static size_t plan_rows_bytes(const SparseMlaParams* p) {
@@ -1367,7 +1424,7 @@ static size_t plan_rows_bytes(const SparseMlaParams* p) {
 static size_t partial_bytes(const SparseMlaParams* p, const Split& split) {
   const int64_t tiles = (int64_t)p->T * (p->H / p->BM);
   if (split.parts < 2) return 0;
-  return (size_t)(tiles - split.split_from) * (size_t)split.parts * (size_t)(p->BM * p->D + p->BM * p->BM / 8) * 4;
+  return (size_t)(tiles - split.split_from) * (size_t)split.parts * (size_t)record_bytes_per_part(p);
 }
 static size_t plan_bytes(const SparseMlaParams* p) {
   return round256(plan_count_bytes(p->T) + plan_rows_bytes(p)) + partial_bytes(p, choose_split(p));
@@ -1395,19 +1452,19 @@ static int device_cus() {
 template <int DT, int D, int NQ, int NP>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
-  if (a.plan_rows != nullptr) {
-    // Plan kernel, then the persistent kernel over the plan when keys are
-    // split into parts or every CU gets at least two items (the persistent
-    // form removes the per-item start, which outweighs a second kernel only
-    // then) and its row-list ring fits next to its KV ring, then the merge of
-    // split keys. Short streams (at most four items per CU, rows mostly from
-    // HBM) use a 4-tile ring with two chunks in flight, long ones 3 tiles.
-    // Otherwise the one-item-per-workgroup kernel resolves its rows.
+  const int64_t tiles = (int64_t)a.T * (a.H / a.BM);
+  if (a.plan_rows != nullptr && a.parts == 1) {
+    // Plan kernel, then the persistent kernel over the plan when every CU gets
+    // at least two items (the persistent form removes the per-item start,
+    // which outweighs a second kernel only then) and its row-list ring fits
+    // next to its KV ring. Short streams (at most four items per CU, rows
+    // mostly from HBM) use a 4-tile ring with two chunks in flight, long ones
+    // 3 tiles. Otherwise (and for split keys) the one-item-per-workgroup kernel
+    // resolves its own rows.
     static int cus = 0;
     if (cus == 0) cus = device_cus();
-    const int64_t tiles = (int64_t)a.T * (a.H / a.BM);
-    const int64_t items = a.split_from + (tiles - a.split_from) * a.parts;
-    if (a.parts > 1 || items >= 2 * (int64_t)cus) {
+    const int64_t items = tiles;
+    if (items >= 2 * (int64_t)cus) {
       const int64_t per_cu = (items + cus - 1) / cus;
       const bool deep = per_cu <= 4 && fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>, 5 * lds) == AFA_OK;
       if (deep || fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>, 4 * lds) == AFA_OK) {
@@ -1422,25 +1479,27 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
         else
           hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64),
                              4 * lds, stream, a);
-        if (a.parts < 2) return (int)hipGetLastError();
-        const hipError_t e2 = hipGetLastError();
-        if (e2 != hipSuccess) return (int)e2;
-        hipLaunchKernelGGL((sparse_merge_kernel<DT, D, NQ, NP>), dim3((unsigned)((tiles - a.split_from) * NP * NQ)),
-                           dim3(merge_threads<D, NP>()), 0, stream, a);
         return (int)hipGetLastError();
       }
     }
   }
-  // One workgroup per item: a 4-tile ring (two chunks in flight) where it
-  // fits, since the kernel runs short streams whose rows mostly come from HBM.
-  const unsigned blocks = (unsigned)a.T * (unsigned)(a.H / a.BM);
+  // One workgroup per item (whole keys, then the parts of split keys): a
+  // 4-tile ring (two chunks in flight) where it fits, since the kernel runs
+  // short streams whose rows mostly come from HBM; then the merge of split keys.
+  const int64_t items = a.split_from + (tiles - a.split_from) * a.parts;
+  const unsigned blocks = (unsigned)items;
   if (fits_lds(sparse_mla_kernel<DT, D, NQ, NP, 4>, lds) == AFA_OK) {
     hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 4>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
-    return (int)hipGetLastError();
+  } else {
+    const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP, 3>, lds);
+    if (fit) return fit;
+    hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 3>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   }
-  const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP, 3>, lds);
-  if (fit) return fit;
-  hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 3>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
+  if (a.parts < 2) return (int)hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((sparse_merge_kernel<DT, D, NQ, NP>), dim3((unsigned)((tiles - a.split_from) * NP * NQ)),
+                     dim3(merge_threads<D, NP>()), 0, stream, a);
   return (int)hipGetLastError();
 }
 
@@ -1479,7 +1538,7 @@ extern "C" int launch_sparse_mla(void* stream, const void* q, const void* ori_kv
     char* w = (char*)workspace;
     a.plan_count = (int32_t*)w;
     a.plan_rows = (uint32_t*)(w + plan_count_bytes(params->T));
-    if (a.parts > 1) a.partials = (float*)(w + round256(plan_count_bytes(params->T) + plan_rows_bytes(params)));
+    if (a.parts > 1) a.partials = w + round256(plan_count_bytes(params->T) + plan_rows_bytes(params));
   } else {
     a.parts = 1;
     a.split_from = a.T * (a.H / a.BM);

@@ -49,13 +49,15 @@ typedef struct SparseMlaParams {
   int32_t WINDOW, TOPK, S, BM;
   int32_t dtype;            /* AFA_DTYPE_* of q, caches and attention_out */
   float scale;              /* SCALE, > 0 */
-  /* Parts each (token, BM-head tile) is split into on the plan path: 0 =
-   * automatic (only the tiles of an incomplete last round over 256 compute
-   * units, where that shortens the longest per-CU stream, e.g. decode-sized
-   * T), 1 = never, 2..8 = every tile. Parts run on different workgroups and
-   * store (running max, denominator, unnormalised O); a merge kernel combines
-   * them in part order, so results are deterministic for a given value. No
-   * counterpart in the reference, whose sizes are compile-time constants. */
+  /* Parts each (token, BM-head tile) key is split into, with a workspace: 0 =
+   * automatic (after at most one full round of keys over 256 compute units,
+   * the keys of the incomplete last round, into the number of parts a cost
+   * model of the GPU finds cheapest, if any: decode with few requests), 1 =
+   * never, 2..8 = every key. Parts run on different workgroups and store their
+   * output normalised by their own denominator, with their running max and
+   * denominator; a merge kernel combines them in part order, so results are
+   * deterministic for a given value. No counterpart in the reference, whose
+   * sizes are compile-time constants. */
   int32_t parts;
   /* Optional debug image of the row selection, NULL normally: int32 [T, S, 2]
    * holding (cache, physical_row) per gather slot, cache 0 = ori_kv,
@@ -80,14 +82,14 @@ typedef struct SparseMlaParams {
  *   seqused_ori_kv i32 [B], seqused_cmp_kv i32 [B], cmp_residual_kv i32 [B],
  *   ori_topk_length i32 [T,1], sinks f32 [H], attention_out [T,H,D] (written).
  * `workspace`: NULL, or at least workspace_size_sparse_mla() bytes of device
- * memory that the call may overwrite. With a workspace, and either at least
- * two work items (token x BM-head tile) per compute unit or tokens split into
- * parts (params->parts), a plan kernel first writes every token's selected-row
- * list into it and a persistent attention kernel streams the items of each
- * compute unit over those lists, and a merge kernel combines split parts;
- * otherwise (or with params->debug_rows set) one workgroup per item resolves
- * its rows itself. With one part, results are bit-identical either way; split
- * tokens differ only in FP32 summation order. */
+ * memory that the call may overwrite. With a workspace and at least two work
+ * items (token x BM-head tile) per compute unit, a plan kernel first writes
+ * every token's selected-row list into it and a persistent attention kernel
+ * streams the items of each compute unit over those lists; otherwise (or with
+ * params->debug_rows set) one workgroup per item (or per part of a split key,
+ * params->parts, whose records a merge kernel then combines in the workspace)
+ * resolves its rows itself. With one part, results are bit-identical either
+ * way; split keys differ only in FP32 summation order. */
 int launch_sparse_mla(void* stream, const void* q, const void* ori_kv, const void* cmp_kv,
                       const int32_t* cmp_sparse_indices, const int32_t* ori_block_table,
                       const int32_t* cmp_block_table, const int32_t* cu_seqlens_q,
@@ -144,7 +146,7 @@ const char* kernel_metadata_simple_attention(void);
 /* workspace_size_<k>: bytes of the optional workspace (sparse_mla: the row-list
  * plan, T * 4 rounded up to 256 plus T * round_up(WINDOW + TOPK, 256) * 4, and
  * with K (token, BM-head tile) keys split into P parts, rounded up to 256,
- * plus K * P * (BM * D + BM * BM / 8) * 4 bytes of partial results; 0 for the
+ * plus K * P * (2 * BM * D + BM * BM / 2) bytes of partial results; 0 for the
  * two dense kernels); returns -1 on a NULL pointer and the
  * launcher's status for invalid sparse parameters (src/backend/workspace.py:100-130). */
 int workspace_size_sparse_mla(uint64_t* bytes, const SparseMlaParams* params);

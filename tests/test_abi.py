@@ -50,16 +50,18 @@ def test_kernel_config_and_workspace_queries(lib):
     params = good_params(T=100, TOPK=1000, S=1128, parts=1)
     assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
     assert size.value == 512 + 100 * 1280 * 4
-    # Split keys add partial records: (split keys) * P * (BM * D + BM * BM / 8)
-    # floats. Automatically only the keys of an incomplete last round of 256
-    # are split, into min(8, 256 / leftover) parts, and only where that saves
-    # more than the merge's cost of 10 chunk steps: T = 16 (no full round) into
-    # 8 parts, T = 100 with 36 chunks into 2; not decode T = 384 (20 + 10 + 10
-    # against 40 chunk steps) nor T = 512 (two full rounds).
-    per_part = (64 * 512 + 64 * 64 // 8) * 4
+    # Split keys add partial records: (split keys) * P * (2 * BM * D + BM * BM / 2)
+    # bytes (normalised b16 outputs plus FP32 max and denominator). Only streams
+    # of at most one full round of 256 keys split, the keys beyond the full
+    # round into the P (r P <= 256) that the library's cost model finds
+    # cheapest, if any beats the whole round: T = 16 into 7 parts (3 chunks
+    # each), T = 100 with 36 chunks into 2; not decode T = 384 (128 keys beyond
+    # the round: HBM-bound parts plus the merge cost more than 20 latency-bound
+    # steps) or T = 512 (two full rounds).
+    per_part = 2 * 64 * 512 + 64 * 64 // 2
     params = good_params()
     assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
-    assert size.value == 49408 + 16 * 8 * per_part
+    assert size.value == 49408 + 16 * 7 * per_part
     params = good_params(T=100, TOPK=1000, S=1128)
     assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(params)) == 0
     assert size.value == 512512 + 100 * 2 * per_part

@@ -77,10 +77,11 @@ def test_validation_cases_match_oracle(device, case, variant):
         assert np.all(actual == 0)
     # Without the debug image the call gets a plan workspace. With one part at
     # this size (fewer than two work items per CU) rows are still resolved
-    # in-kernel: the same bits. By default (None) the library splits each token
-    # over eight workgroups here (no full round of 256 tiles: plan, persistent
-    # and merge kernels); 2, 3 and 8 parts cover other merge widths, with
-    # masked placeholder parts where a token has fewer chunks than parts.
+    # in-kernel: the same bits. By default (None) the library's cost model
+    # splits each token of these small cases over several workgroups (far
+    # fewer keys than CUs: one-item kernel on parts, then the merge kernel);
+    # 2, 3 and 8 parts cover other merge widths, with masked placeholder parts
+    # where a token has fewer chunks than parts.
     from ascendflow_amd.sparse_attention import sparse_mla
 
     fused = tensors["attention_out"].clone()
@@ -111,8 +112,7 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
     its output must equal the in-kernel row resolution bit for bit; with the
     tokens split over 2 or 4 workgroups (partial results merged, 3-tile ring)
     it must match the oracle on a sample that includes empty and one-row
-    selections. By default (None) the 32 (BM = 64) or 64 (BM = 32) tiles of
-    the incomplete third or fifth round are split and merged."""
+    selections (the split runs on the one-item kernel, then the merge)."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
     policy = sr.default_policy(B=6, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
