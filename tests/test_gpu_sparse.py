@@ -210,6 +210,36 @@ def test_decode_b64x6_ctx128k_all_tokens(device):
 
 
 
+@pytest.mark.parametrize("batch", [1, 4, 48])
+def test_decode_small_batches_split_automatically(device, batch):
+    """Decode with few requests (x 6 queries at 128K): the library splits the
+    keys beyond the last full round of 256 into parts (B1 and B4: every key,
+    7 and 5 parts; B48: the 32 keys after a full round, 5 parts, launched
+    after the whole keys and mapped to XCDs as their own segment) and merges
+    them. Outputs and softmax_lse must match the oracle on a sample covering
+    whole and split keys; the debug call (no split) must agree within the
+    same tolerance and select the oracle's rows."""
+    from ascendflow_amd.sparse_attention import sparse_mla
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+
+    print(f"\n[sparse] decode B{batch}x6 ctx 131072 (automatic split)", flush=True)
+    policy = measurement_policy(batch=batch, query_tokens=6, context=131072)
+    inputs = make_inputs(policy, 131072, device=device)
+    T = policy["T"]
+    rng = np.random.default_rng(batch)
+    tokens = sorted({0, T - 1, *rng.choice(T, min(T, 24), replace=False).tolist()}
+                    | ({255, 256, 257, 270, 287} if T > 256 else set()))
+    check_measured(inputs, tokens, device, split=True)
+    lse = torch.full((T, policy["H"]), float("nan"), dtype=torch.float32, device=device)
+    sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), softmax_lse=lse)
+    torch.cuda.synchronize()
+    data = host_view(inputs, tokens)
+    index = torch.as_tensor(tokens, device=device)
+    assert_lse(lse[index], sr.oracle_lse(data, policy, tokens))
+    assert_close(inputs.tensors["attention_out"][index].float().cpu().numpy(), sr.oracle_fp32(data, policy, tokens),
+                 policy["DTYPE"])
+
+
 def test_prefill_q8k_ctx32k_sampled_tokens(device):
     """Prefill configuration on a spread sample of tokens."""
     from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
