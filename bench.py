@@ -230,7 +230,8 @@ def main():
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the sparse-MLA path shards by query token with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the sparse-MLA path shards by query token with no exchange, so N GPUs run N independent "
+              "token shards; only the one-GPU share is measured here)", file=sys.stderr)
         return 2
 
     import torch
