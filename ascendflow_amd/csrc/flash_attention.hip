@@ -54,6 +54,12 @@ struct FaArgs {
 // that reach the tail or the diagonal.
 constexpr float FA_TAU = 8.0f;
 constexpr int FA_NSTAGE = 3;
+// Progress-ordered wave priorities: a wave starts each chunk at priority 3
+// and steps down at half of QK, after QK and at half of PV, so of the two waves
+// sharing a SIMD the one behind wins the MFMA arbitration (otherwise the older
+// wave always wins, finishes first and waits at the barrier while the other
+// runs alone).
+constexpr bool FA_PROGRESS_PRIO = true;
 
 template <int DT, int NW, int QT>
 __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
@@ -283,6 +289,7 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       pf[qt][h][(t & 1) * 4 + i] = (scalar)p;
     };
     auto qk_between = [&](int f) {
+      if (FA_PROGRESS_PRIO && f == QK_FRAGS / 2 - 1) __builtin_amdgcn_s_setprio(2);
       if (f < QT) {
         float m = -INFINITY;
 #pragma unroll
@@ -318,6 +325,7 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       }
     };
     auto pv_between = [&](int f) {
+      if (FA_PROGRESS_PRIO && f == PV_FRAGS / 2 - 1) __builtin_amdgcn_s_setprio(0);
       if (f < PV_EXP_STEPS) {
 #pragma unroll
         for (int e = 0; e < HALF; ++e)
@@ -331,7 +339,9 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
     // The last chunk also runs a QK, over the stale tile (c + 1) % 3 (no load
     // is in flight into it), so that the softmax has one code path; those
     // scores are never read.
+    if (FA_PROGRESS_PRIO) __builtin_amdgcn_s_setprio(3);
     qk_chunk(c + 1, nxt, qk_between);
+    if (FA_PROGRESS_PRIO) __builtin_amdgcn_s_setprio(1);
     pv_chunk(c, pf, pv_between);
   };
   for (int c = 0; c < chunks; c += 2) {
