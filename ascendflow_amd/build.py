@@ -32,6 +32,12 @@ HIP_FLAGS = (
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # Device code holds no NaNs (masked scores are -inf, never NaN): without
+    # this, every fmaxf on a value the compiler cannot prove canonical (MFMA
+    # results, lane swaps) gets an extra v_max_f32 x, x to quiet signalling
+    # NaNs. Host code keeps IEEE NaN semantics (the launchers' argument checks).
+    "-Xarch_device",
+    "-fno-honor-nans",
     f"-I{ROOT / 'include'}",
 )
 

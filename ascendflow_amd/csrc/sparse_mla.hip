@@ -643,18 +643,26 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       const int slot = i & 1;
       float x0[4], x1[4];
       float cmax = -INFINITY;
-      const int live = placeholder ? 0 : n_rows - list_chunk(i) * CHUNK;
+      // Uniform (readfirstlane): the mask below is then a scalar branch that
+      // full chunks skip, not per-element selects on every chunk.
+      const int live = __builtin_amdgcn_readfirstlane(placeholder ? 0 : n_rows - list_chunk(i) * CHUNK);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         x0[k] = s0[k];
         x1[k] = s1[k];
-        if (live < CHUNK) {
+      }
+      if (live < CHUNK) {
+        // The empty asm keeps this a branch (it is not speculated into selects).
+        __asm__ volatile("");
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
           const int row = sigma(4 * g + k);
           x0[k] = (row < live) ? x0[k] : -INFINITY;
           x1[k] = (16 + row < live) ? x1[k] : -INFINITY;
         }
-        cmax = fmaxf(cmax, fmaxf(x0[k], x1[k]));
       }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cmax = fmaxf(cmax, fmaxf(x0[k], x1[k]));
       cmax = max_over_lane_groups(cmax);
       const float m_new = fmaxf(m_run, cmax * scale_log2);
       const bool raise = __ballot(m_new > m_run + TAU) != 0ull;
@@ -1031,18 +1039,27 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       float x0[4], x1[4];
       float cmax = -INFINITY;
       // Rows of this chunk that hold selected entries (<= 0: masked placeholder).
-      const int live = cur.n > 0 ? count_lds[cur.j % LISTS] - (cur.first + cur.c) * CHUNK : 0;
+      // Uniform (readfirstlane): the mask below is then a scalar branch that
+      // full chunks skip, not per-element selects on every chunk.
+      const int live =
+          __builtin_amdgcn_readfirstlane(cur.n > 0 ? count_lds[cur.j % LISTS] - (cur.first + cur.c) * CHUNK : 0);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         x0[k] = s0[k];
         x1[k] = s1[k];
-        if (live < CHUNK) {
+      }
+      if (live < CHUNK) {
+        // The empty asm keeps this a branch (it is not speculated into selects).
+        __asm__ volatile("");
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
           const int row = sigma(4 * g + k);
           x0[k] = (row < live) ? x0[k] : -INFINITY;
           x1[k] = (16 + row < live) ? x1[k] : -INFINITY;
         }
-        cmax = fmaxf(cmax, fmaxf(x0[k], x1[k]));
       }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cmax = fmaxf(cmax, fmaxf(x0[k], x1[k]));
       cmax = max_over_lane_groups(cmax);
       const float m_new = fmaxf(m_run, cmax * scale_log2);
       const bool raise = __ballot(m_new > m_run + TAU) != 0ull;
