@@ -15,9 +15,9 @@
 //      persistent form (sparse_mla_persistent_kernel) streams the tokens of
 //      each CU through one pipeline, so the three dependent global round trips
 //      and the pipeline fill no longer idle the matrix cores at token starts;
-//   2. stream the listed rows through a 3-stage ring of XOR-swizzled LDS
-//      tiles of CHUNK rows with the load-to-LDS path (global_load_lds_dwordx4,
-//      one wave load per 1 KiB row when D = 512);
+//   2. stream the listed rows through a 3- or 4-stage ring of XOR-swizzled
+//      LDS tiles of CHUNK rows with the load-to-LDS path
+//      (global_load_lds_dwordx4, one wave load per 1 KiB row when D = 512);
 //   3. score waves (16 heads each, all D features of Q resident in registers):
 //      S^T[rows, heads] = KV * Q^T on v_mfma_f32_16x16x32_{bf16,f16}, FP32
 //      online softmax in the exp2 domain (the sink seeds the running max and
@@ -26,7 +26,10 @@
 //   4. output waves (all heads, D/NP features each): O^T[d, heads] +=
 //      V^T * P^T, V^T fragments from the same LDS rows through
 //      ds_read_b64_tr_b16;
-//   5. O = O_acc * (1 / l), rounded to the storage dtype.
+//   5. O = O_acc * (1 / l), rounded to the storage dtype. Keys of a short
+//      last round may instead be split over several workgroups by list
+//      chunks; each part stores its normalised output with its running max
+//      and denominator, and sparse_merge_kernel combines the parts.
 //
 // K and V are the same gathered rows; each row is read from global memory
 // once per workgroup and from LDS once per score wave and once per output wave.
@@ -70,7 +73,7 @@ struct SparseArgs {
   void* partials;        // workspace: [split keys][parts][output waves] records (store_record)
   int32_t B, T, H, D, PAGE, RATIO, table_width, ori_blocks, cmp_blocks, WINDOW, TOPK, S, BM;
   int32_t list_pad;      // row-list capacity: WINDOW + TOPK rounded up to 256 (whole KiB)
-  int32_t parts;         // parts each split (token, head tile) is divided into (persistent kernel)
+  int32_t parts;         // parts each split (token, head tile) key is divided into (one-item kernel)
   int32_t split_from;    // first split (token, head tile) key; keys below it run whole
   float scale;
 };
@@ -771,8 +774,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   }
 }
 
-// Stream position: chunk c of work item j (workgroup-local index), whose part
-// starts at list chunk `first` and holds n list chunks (0: one masked chunk).
+// Stream position: chunk c of work item j (workgroup-local index), whose
+// chunks are list chunks first .. first + n - 1 (n = 0: one masked chunk).
 struct Cursor {
   int j, c, first, n;
   __device__ __forceinline__ int chunks() const { return n > 0 ? n : 1; }
@@ -792,7 +795,7 @@ struct Cursor {
 //    starts and issue no other vector memory loads, so those loads have a
 //    whole item to land (vector loads of a wave complete in issue order, so a
 //    score-wave KV fetch would wait for them);
-//  - each item's running max starts at its sinks (part 0 alone counts the
+//  - each item's running max starts at its sinks (one lane group counts the
 //    sink's e^(sink - m)), its output accumulators are cleared on its first PV
 //    step, and its running max and denominator travel through LDS slot item & 1.
 // The first item's Q goes through LDS as in sparse_mla_kernel.
