@@ -788,7 +788,7 @@ struct Cursor {
 // pipeline drain and no dependent global round trip.
 //  - the KV ring of NS tiles, P slots and step parities run on across items;
 //    output waves fetch KV rows AHEAD = NS - 2 chunks ahead of the score waves
-//    (two chunks in flight hide the HBM latency of short streams);
+//    (the host launches the 3-tile ring, one chunk in flight);
 //  - output waves copy the row list (and count) of item j + LISTS - 1 when
 //    item j starts, into a ring of LISTS LDS lists;
 //  - score waves load Q and the sinks of item j + 1 into registers when item j
@@ -1485,30 +1485,23 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
     // Plan kernel, then the persistent kernel over the plan when every CU gets
     // at least two items (the persistent form removes the per-item start,
     // which outweighs a second kernel only then) and its row-list ring fits
-    // next to its KV ring. Short streams (at most four items per CU, rows
-    // mostly from HBM) use a 4-tile ring with two chunks in flight, long ones
-    // 3 tiles. Otherwise (and for split keys) the one-item-per-workgroup kernel
-    // resolves its own rows.
+    // next to its KV ring. The 3-tile ring leaves room for the staged output
+    // stores; with them and the role priorities it measured faster than the
+    // 4-tile ring at every stream length (decode B86, B128 and B170 x 6: 1%,
+    // 4% and 1%). Otherwise (and for split keys) the one-item-per-workgroup
+    // kernel resolves its own rows.
     static int cus = 0;
     if (cus == 0) cus = device_cus();
     const int64_t items = tiles;
-    if (items >= 2 * (int64_t)cus) {
-      const int64_t per_cu = (items + cus - 1) / cus;
-      const bool deep = per_cu <= 4 && fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>, 5 * lds) == AFA_OK;
-      if (deep || fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>, 4 * lds) == AFA_OK) {
-        constexpr int PLAN_THREADS = 256;
-        hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return (int)e;
-        const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
-        if (deep)
-          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>), dim3(grid), dim3((NQ + NP) * 64),
-                             5 * lds, stream, a);
-        else
-          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64),
-                             4 * lds, stream, a);
-        return (int)hipGetLastError();
-      }
+    if (items >= 2 * (int64_t)cus && fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>, 4 * lds) == AFA_OK) {
+      constexpr int PLAN_THREADS = 256;
+      hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return (int)e;
+      const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
+      hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64),
+                         4 * lds, stream, a);
+      return (int)hipGetLastError();
     }
   }
   // One workgroup per item (whole keys, then the parts of split keys): a
