@@ -277,8 +277,12 @@ __device__ __forceinline__ PartRange part_range(int count, int part, int parts) 
 template <int NTH>
 __global__ __launch_bounds__(NTH) void sparse_plan_kernel(SparseArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t plan_list[];
-  // Three passes of 256 slots: WINDOW + TOPK = 640 in one round-trip sequence.
-  constexpr int GP = 3;
+  // One wave per token, ten passes of 64 slots: WINDOW + TOPK = 640 in one
+  // round-trip sequence. The kernel is latency-bound (three dependent round
+  // trips per token); one-wave workgroups let every token of a Q8K prefill be
+  // resident at once (four waves per token took ~4 rounds of residency:
+  // prefill 0.7-1.2% slower).
+  constexpr int GP = 10;
   __shared__ int wave_count[GP][NTH / 64];
   __shared__ int request_scratch[NTH / 64];
   const int token = blockIdx.x;
@@ -1494,7 +1498,7 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
     if (cus == 0) cus = device_cus();
     const int64_t items = tiles;
     if (items >= 2 * (int64_t)cus && fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>, 4 * lds) == AFA_OK) {
-      constexpr int PLAN_THREADS = 256;
+      constexpr int PLAN_THREADS = 64;
       hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
       const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return (int)e;
