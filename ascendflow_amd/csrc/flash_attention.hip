@@ -47,12 +47,15 @@ struct FaArgs {
 // Online softmax (attention.py:73-139) in FP32 registers, exp2 domain: the
 // chunk max is taken on raw scores (the scale is positive) and the scale goes
 // into the exponent's FMA; the running max is raised, with O and l rescaled
-// by alpha = 2^(m - m'), only when some query's max exceeds it by more than
-// FA_TAU, so P <= 2^FA_TAU; O / l is independent of the reference point.
+// by alpha = 2^(m - m'), whenever some query's max grows (FA_TAU = 0), so
+// P <= 1 and the key holding the running max gets P = 1 exactly, as in the
+// reference's recurrence. A lazily raised reference point (P up to 2^TAU)
+// rounds the dominant key's P to the storage dtype instead; with bf16 (8-bit
+// mantissa) and sharp scores that alone moved outputs by 2 ulps.
 // Masks (attention.py:96-110): keys >= Sk, and for causal attention key j is
 // visible to query i iff j <= i (top-left); they are applied only in chunks
 // that reach the tail or the diagonal.
-constexpr float FA_TAU = 8.0f;
+constexpr float FA_TAU = 0.0f;
 constexpr int FA_NSTAGE = 3;
 // Progress-ordered wave priorities: a wave starts each chunk at priority 3
 // and steps down at half of QK, after QK and at half of PV, so of the two waves
@@ -554,26 +557,41 @@ extern "C" int workspace_size_simple_attention(uint64_t* bytes, int64_t S, int64
   return AFA_OK;
 }
 
+// Launch-ABI descriptions in the reference's metadata schema
+// (src/backend/abi.py:19-59): tensors (dtype, shape with named axes, layout,
+// access), runtime size parameters with minimum and multiple, workspace flag.
+// The FA sizes the reference specialises at compile time (B, HQ, HKV, D,
+// dtype, causal, scale) travel in FaParams ("params_struct"); "DTYPE" is one
+// of "dtypes".
 extern "C" const char* kernel_metadata_attention_target(void) {
-  return "{\"version\":1,\"kernel\":\"attention_target\",\"tensors\":["
+  return "{\"version\":1,\"name\":\"attention_target\",\"target\":\"gfx950\",\"kind\":\"mixed\","
+         "\"groups\":256,\"disjoint_external\":true,\"device_resources\":null,"
+         "\"dtypes\":{\"DTYPE\":[\"f16\",\"bf16\"]},\"tensors\":["
          "{\"name\":\"Q\",\"dtype\":\"DTYPE\",\"shape\":[\"B\",\"HQ\",\"Sq\",\"D\"],"
-         "\"access\":\"read\"},"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
          "{\"name\":\"K\",\"dtype\":\"DTYPE\",\"shape\":[\"B\",\"HKV\",\"Sk\",\"D\"],"
-         "\"access\":\"read\"},"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
          "{\"name\":\"V\",\"dtype\":\"DTYPE\",\"shape\":[\"B\",\"HKV\",\"Sk\",\"D\"],"
-         "\"access\":\"read\"},"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
          "{\"name\":\"O\",\"dtype\":\"DTYPE\",\"shape\":[\"B\",\"HQ\",\"Sq\",\"D\"],"
-         "\"access\":\"write\"}],"
-         "\"parameters\":[{\"name\":\"Sq\",\"minimum\":1},{\"name\":\"Sk\",\"minimum\":1}],"
-         "\"disjoint_external\":true,\"workspace\":false}";
+         "\"layout\":\"linear\",\"access\":\"write\"}],"
+         "\"parameters\":[{\"name\":\"Sq\",\"minimum\":1,\"multiple\":1},"
+         "{\"name\":\"Sk\",\"minimum\":1,\"multiple\":1}],"
+         "\"params_struct\":{\"name\":\"FaParams\",\"fields\":[\"B\",\"HQ\",\"HKV\",\"D\",\"dtype\","
+         "\"causal\",\"scale\",\"reserved\"]},"
+         "\"workspace\":false}";
 }
-
 extern "C" const char* kernel_metadata_simple_attention(void) {
-  return "{\"version\":1,\"kernel\":\"simple_attention\",\"tensors\":["
-         "{\"name\":\"Q\",\"dtype\":\"f16\",\"shape\":[\"H\",\"S\",128],\"access\":\"read\"},"
-         "{\"name\":\"K\",\"dtype\":\"f16\",\"shape\":[\"H\",128,128],\"access\":\"read\"},"
-         "{\"name\":\"V\",\"dtype\":\"f16\",\"shape\":[\"H\",128,128],\"access\":\"read\"},"
-         "{\"name\":\"O\",\"dtype\":\"f16\",\"shape\":[\"H\",\"S\",128],\"access\":\"write\"}],"
+  return "{\"version\":1,\"name\":\"simple_attention\",\"target\":\"gfx950\",\"kind\":\"mixed\","
+         "\"groups\":256,\"disjoint_external\":true,\"device_resources\":null,\"tensors\":["
+         "{\"name\":\"Q\",\"dtype\":\"f16\",\"shape\":[\"H\",\"S\",128],\"layout\":\"linear\","
+         "\"access\":\"read\"},"
+         "{\"name\":\"K\",\"dtype\":\"f16\",\"shape\":[\"H\",128,128],\"layout\":\"linear\","
+         "\"access\":\"read\"},"
+         "{\"name\":\"V\",\"dtype\":\"f16\",\"shape\":[\"H\",128,128],\"layout\":\"linear\","
+         "\"access\":\"read\"},"
+         "{\"name\":\"O\",\"dtype\":\"f16\",\"shape\":[\"H\",\"S\",128],\"layout\":\"linear\","
+         "\"access\":\"write\"}],"
          "\"parameters\":[{\"name\":\"S\",\"minimum\":64,\"multiple\":64},"
-         "{\"name\":\"H\",\"minimum\":1}],\"disjoint_external\":true,\"workspace\":false}";
+         "{\"name\":\"H\",\"minimum\":1,\"multiple\":1}],\"workspace\":false}";
 }

@@ -35,6 +35,7 @@
 // once per workgroup and from LDS once per score wave and once per output wave.
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "../../include/ascendflow_amd.h"
@@ -486,14 +487,18 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     if (tid < padded - n_rows) row_list[n_rows + tid] = row_list[0];
     // A part of an empty selection streams one masked chunk of ori row 0.
     if (split && n_rows == 0 && tid < CHUNK) row_list[tid] = 0u;
-    if (a.debug_rows != nullptr && head0 == 0) {
-      const int slots = a.WINDOW + geo.count_cmp;
-      for (int s = tid; s < a.S; s += NT) {
-        uint32_t e = 0;
-        const bool v = s < slots && resolve_slot(a, geo, token, s, e);
-        int2 r = make_int2(-1, -1);
-        if (v) r = make_int2((e & CMP_BIT) ? 1 : 0, (int)(e & ~CMP_BIT));
-        ((int2*)a.debug_rows)[(size_t)token * a.S + s] = r;
+    if (a.debug_rows != nullptr && head0 == 0 && part == 0) {
+      // The compacted list this workgroup streams, entry r < n_rows as
+      // (cache, physical row), then (-1, -1). Entries below n_rows are final
+      // (resolve_rows ended with a barrier); the padding writes above touch
+      // only entries from n_rows on.
+      for (int r = tid; r < a.S; r += NT) {
+        int2 v = make_int2(-1, -1);
+        if (r < n_rows) {
+          const uint32_t e = row_list[r];
+          v = make_int2((e & CMP_BIT) ? 1 : 0, (int)(e & ~CMP_BIT));
+        }
+        ((int2*)a.debug_rows)[(size_t)token * a.S + r] = v;
       }
     }
     block_barrier();
@@ -1334,6 +1339,9 @@ static int check_sparse(const SparseMlaParams* p) {
   if (p->PAGE <= 0 || (p->RATIO != 1 && p->RATIO != 2) || p->PAGE % p->RATIO) return AFA_E_SHAPE;
   if (p->MAX_SEQ <= 0 || p->MAX_SEQ % p->PAGE) return AFA_E_SHAPE;
   if (p->WINDOW < 0 || p->WINDOW > 4096 || p->TOPK < 0 || p->TOPK > 8192) return AFA_E_SHAPE;
+  // At least one gather slot: the row lists (workspace and LDS) are sized by
+  // WINDOW + TOPK, and every token streams at least one chunk.
+  if (p->WINDOW + p->TOPK < 1) return AFA_E_SHAPE;
   if (p->S < p->WINDOW + p->TOPK) return AFA_E_SHAPE;
   if (p->ORI_BLOCKS <= 0 || p->CMP_BLOCKS <= 0) return AFA_E_SHAPE;
   if ((int64_t)p->ORI_BLOCKS * p->PAGE >= (int64_t)CMP_BIT) return AFA_E_SHAPE;
@@ -1465,12 +1473,17 @@ static size_t plan_bytes(const SparseMlaParams* p) {
 // LDS of one workgroup (the KV ring, P slots and the row list) must fit the
 // 160 KiB a gfx950 CU holds.
 constexpr size_t LDS_BYTES = 160 * 1024;
-template <typename K>
-static int fits_lds(K kernel, size_t dynamic_bytes) {
-  hipFuncAttributes attr;
-  const hipError_t e = hipFuncGetAttributes(&attr, (const void*)kernel);
-  if (e != hipSuccess) return (int)e;
-  return attr.sharedSizeBytes + dynamic_bytes <= LDS_BYTES ? AFA_OK : AFA_E_SHAPE;
+// The static LDS of each kernel is queried once per process (a function-local
+// static per kernel, initialised thread-safely) instead of on every launch.
+template <auto Kernel>
+static int fits_lds(size_t dynamic_bytes) {
+  static const std::pair<hipError_t, size_t> info = [] {
+    hipFuncAttributes attr{};
+    const hipError_t e = hipFuncGetAttributes(&attr, (const void*)Kernel);
+    return std::make_pair(e, (size_t)attr.sharedSizeBytes);
+  }();
+  if (info.first != hipSuccess) return (int)info.first;
+  return info.second + dynamic_bytes <= LDS_BYTES ? AFA_OK : AFA_E_SHAPE;
 }
 
 // Compute units of the current device (one persistent workgroup each).
@@ -1494,10 +1507,9 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
     // 4-tile ring at every stream length (decode B86, B128 and B170 x 6: 1%,
     // 4% and 1%). Otherwise (and for split keys) the one-item-per-workgroup
     // kernel resolves its own rows.
-    static int cus = 0;
-    if (cus == 0) cus = device_cus();
+    static const int cus = device_cus();
     const int64_t items = tiles;
-    if (items >= 2 * (int64_t)cus && fits_lds(sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>, 4 * lds) == AFA_OK) {
+    if (items >= 2 * (int64_t)cus && fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>>(4 * lds) == AFA_OK) {
       constexpr int PLAN_THREADS = 64;
       hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
       const hipError_t e = hipGetLastError();
@@ -1513,10 +1525,10 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   // short streams whose rows mostly come from HBM; then the merge of split keys.
   const int64_t items = a.split_from + (tiles - a.split_from) * a.parts;
   const unsigned blocks = (unsigned)items;
-  if (fits_lds(sparse_mla_kernel<DT, D, NQ, NP, 4>, lds) == AFA_OK) {
+  if (fits_lds<sparse_mla_kernel<DT, D, NQ, NP, 4>>(lds) == AFA_OK) {
     hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 4>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   } else {
-    const int fit = fits_lds(sparse_mla_kernel<DT, D, NQ, NP, 3>, lds);
+    const int fit = fits_lds<sparse_mla_kernel<DT, D, NQ, NP, 3>>(lds);
     if (fit) return fit;
     hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 3>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   }
@@ -1620,26 +1632,46 @@ extern "C" int workspace_size_sparse_mla(uint64_t* bytes, const SparseMlaParams*
   return AFA_OK;
 }
 
+// Launch-ABI description in the reference's metadata schema
+// (src/backend/abi.py:19-59): tensors with dtype, shape (named axes, bound
+// consistently across tensors by the caller), layout and access; runtime
+// size parameters with minimum and multiple (none here: the reference
+// specialises every sparse size at compile time, and this library takes them
+// in SparseMlaParams, listed under "params_struct"); "DTYPE" is one of
+// "dtypes". CMP_PAGE = PAGE / RATIO, TABLE_WIDTH = MAX_SEQ / PAGE, B1 = B + 1.
 extern "C" const char* kernel_metadata_sparse_mla(void) {
-  return "{\"version\":1,\"kernel\":\"sparse_mla\",\"tensors\":["
-         "{\"name\":\"q\",\"dtype\":\"DTYPE\",\"shape\":[\"T\",\"H\",\"D\"],\"access\":\"read\"},"
+  return "{\"version\":1,\"name\":\"sparse_mla\",\"target\":\"gfx950\",\"kind\":\"mixed\","
+         "\"groups\":256,\"disjoint_external\":true,\"device_resources\":null,"
+         "\"dtypes\":{\"DTYPE\":[\"bf16\",\"f16\"]},\"tensors\":["
+         "{\"name\":\"q\",\"dtype\":\"DTYPE\",\"shape\":[\"T\",\"H\",\"D\"],\"layout\":\"linear\","
+         "\"access\":\"read\"},"
          "{\"name\":\"ori_kv\",\"dtype\":\"DTYPE\",\"shape\":[\"ORI_BLOCKS\",\"PAGE\",1,\"D\"],"
-         "\"access\":\"read\"},"
-         "{\"name\":\"cmp_kv\",\"dtype\":\"DTYPE\",\"shape\":[\"CMP_BLOCKS\",\"PAGE/RATIO\",1,\"D\"],"
-         "\"access\":\"read\"},"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
+         "{\"name\":\"cmp_kv\",\"dtype\":\"DTYPE\",\"shape\":[\"CMP_BLOCKS\",\"CMP_PAGE\",1,\"D\"],"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
          "{\"name\":\"cmp_sparse_indices\",\"dtype\":\"i32\",\"shape\":[\"T\",1,\"TOPK\"],"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
+         "{\"name\":\"ori_block_table\",\"dtype\":\"i32\",\"shape\":[\"B\",\"TABLE_WIDTH\"],"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
+         "{\"name\":\"cmp_block_table\",\"dtype\":\"i32\",\"shape\":[\"B\",\"TABLE_WIDTH\"],"
+         "\"layout\":\"linear\",\"access\":\"read\"},"
+         "{\"name\":\"cu_seqlens_q\",\"dtype\":\"i32\",\"shape\":[\"B1\"],\"layout\":\"linear\","
          "\"access\":\"read\"},"
-         "{\"name\":\"ori_block_table\",\"dtype\":\"i32\",\"shape\":[\"B\",\"MAX_SEQ/PAGE\"],"
+         "{\"name\":\"seqused_ori_kv\",\"dtype\":\"i32\",\"shape\":[\"B\"],\"layout\":\"linear\","
          "\"access\":\"read\"},"
-         "{\"name\":\"cmp_block_table\",\"dtype\":\"i32\",\"shape\":[\"B\",\"MAX_SEQ/PAGE\"],"
+         "{\"name\":\"seqused_cmp_kv\",\"dtype\":\"i32\",\"shape\":[\"B\"],\"layout\":\"linear\","
          "\"access\":\"read\"},"
-         "{\"name\":\"cu_seqlens_q\",\"dtype\":\"i32\",\"shape\":[\"B+1\"],\"access\":\"read\"},"
-         "{\"name\":\"seqused_ori_kv\",\"dtype\":\"i32\",\"shape\":[\"B\"],\"access\":\"read\"},"
-         "{\"name\":\"seqused_cmp_kv\",\"dtype\":\"i32\",\"shape\":[\"B\"],\"access\":\"read\"},"
-         "{\"name\":\"cmp_residual_kv\",\"dtype\":\"i32\",\"shape\":[\"B\"],\"access\":\"read\"},"
-         "{\"name\":\"ori_topk_length\",\"dtype\":\"i32\",\"shape\":[\"T\",1],\"access\":\"read\"},"
-         "{\"name\":\"sinks\",\"dtype\":\"f32\",\"shape\":[\"H\"],\"access\":\"read\"},"
+         "{\"name\":\"cmp_residual_kv\",\"dtype\":\"i32\",\"shape\":[\"B\"],\"layout\":\"linear\","
+         "\"access\":\"read\"},"
+         "{\"name\":\"ori_topk_length\",\"dtype\":\"i32\",\"shape\":[\"T\",1],\"layout\":\"linear\","
+         "\"access\":\"read\"},"
+         "{\"name\":\"sinks\",\"dtype\":\"f32\",\"shape\":[\"H\"],\"layout\":\"linear\","
+         "\"access\":\"read\"},"
          "{\"name\":\"attention_out\",\"dtype\":\"DTYPE\",\"shape\":[\"T\",\"H\",\"D\"],"
-         "\"access\":\"write\"}],"
-         "\"parameters\":\"SparseMlaParams\",\"disjoint_external\":true,\"workspace\":true}";
+         "\"layout\":\"linear\",\"access\":\"write\"}],"
+         "\"parameters\":[],"
+         "\"params_struct\":{\"name\":\"SparseMlaParams\",\"fields\":[\"B\",\"T\",\"H\",\"D\","
+         "\"PAGE\",\"RATIO\",\"MAX_SEQ\",\"ORI_BLOCKS\",\"CMP_BLOCKS\",\"WINDOW\",\"TOPK\",\"S\","
+         "\"BM\",\"dtype\",\"scale\",\"parts\",\"debug_rows\",\"softmax_lse\"]},"
+         "\"workspace\":true}";
 }

@@ -129,12 +129,16 @@ def sparse_mla(
     debug_rows=None,
     parts=None,
     softmax_lse=None,
+    workspace=None,
 ):
     """Sparse MLA forward; writes ``attention_out`` [T, H, D] and returns it.
 
-    ``debug_rows`` (optional int32 [T, S, 2] device tensor) receives the
-    kernel's own row selection per gather slot: (cache, physical row),
-    cache 0 = ori_kv, 1 = cmp_kv, (-1, -1) unused.
+    ``debug_rows`` (optional int32 [T, S, 2] device tensor) receives, per
+    token, the compacted row list the kernel then streams: entry r < n is the
+    r-th selected row as (cache, physical row), cache 0 = ori_kv,
+    1 = cmp_kv, in slot order (window positions, then compressed ranks),
+    and (-1, -1) from n on. With it the rows are resolved inside the
+    attention kernel (one workgroup per token and head tile, no split).
 
     ``softmax_lse`` (optional float32 [T, H] device tensor) receives the
     natural-log normaliser ln(sum_j exp(s_j) + exp(sinks[h])) of every
@@ -146,6 +150,14 @@ def sparse_mla(
     into k parts whose partial results a merge kernel combines. By default only
     the tokens of an incomplete last round over the 256 CUs are split, where
     that shortens the longest per-CU stream (decode-sized batches).
+
+    ``workspace`` (optional uint8 device tensor of at least
+    ``workspace_bytes(...)`` bytes) replaces the per-call allocation. When
+    the plan path runs (at least two work items per CU, no split, no debug
+    image), it holds the row-list plan afterwards (``plan_layout``): the
+    selected-row count of every token, then every token's list of tagged
+    rows (bit 31 set for cmp_kv) padded with its first row to whole 32-row
+    chunks (32 entries of ori_kv row 0 for an empty selection).
     """
     dtype = storage_dtype(DTYPE)
     check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PARTS, GROUPS, VR, BK, C, SCALE)
@@ -181,7 +193,13 @@ def sparse_mla(
     # the caching allocator hands it out in stream order, so no host sync.
     nbytes = ct.c_uint64(0)
     _native.check(lib.workspace_size_sparse_mla(ct.byref(nbytes), ct.byref(params)), "workspace_size_sparse_mla")
-    workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=device) if nbytes.value else None
+    if workspace is None:
+        workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=device) if nbytes.value else None
+    else:
+        require(isinstance(workspace, torch.Tensor) and workspace.dtype == torch.uint8 and workspace.is_contiguous()
+                and workspace.device == device, "workspace must be a contiguous uint8 tensor on the operands' device")
+        require(workspace.numel() >= nbytes.value, f"workspace holds {workspace.numel()} bytes, needs {nbytes.value}")
+        check_disjoint([(name, t, False) for name, t in tensors.items()] + [("workspace", workspace, True)])
     status = lib.launch_sparse_mla(
         stream_handle(device),
         *(tensors[name].data_ptr() for name in tensors),
@@ -190,3 +208,24 @@ def sparse_mla(
     )
     _native.check(status, "launch_sparse_mla")
     return attention_out
+
+
+def workspace_bytes(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, DTYPE="bf16",
+                    SCALE=0.04419417382415922, parts=None):
+    """Bytes of the optional workspace of one call (``workspace_size_sparse_mla``)."""
+    params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM,
+                         storage_dtype(DTYPE), SCALE, None, parts or 0, None)
+    nbytes = ct.c_uint64(0)
+    _native.check(_native.library().workspace_size_sparse_mla(ct.byref(nbytes), ct.byref(params)),
+                  "workspace_size_sparse_mla")
+    return int(nbytes.value)
+
+
+def plan_layout(T, WINDOW, TOPK):
+    """Byte offsets of the row-list plan in the workspace: (counts offset,
+    rows offset, entries per token). Counts are int32 [T] at offset 0; the
+    row lists are uint32 [T][entries] from the 256-byte boundary after them,
+    entries = WINDOW + TOPK rounded up to 256 (include/ascendflow_amd.h)."""
+    counts = 0
+    rows = -(-4 * T // 256) * 256
+    return counts, rows, -(-(WINDOW + TOPK) // 256) * 256

@@ -166,49 +166,97 @@ def attention_extras(steps, warmup, flush, device, which=ATTENTION_KEYS, prewarm
     return out
 
 
-def cpu_baseline(result, sample_tokens):
-    """Time the oracle's vectorised FP32 PyTorch-CPU sparse MLA on a token sample."""
-    import numpy as np
-    import torch
+def cpu_threads():
+    """Threads for the CPU baseline: every CPU in this process's affinity mask,
+    capped by the cgroup CPU quota when one is set (more threads than the quota
+    only time-slice). Returns (threads, affinity CPUs, quota or None)."""
+    import math
 
-    from oracle.cpu_reference import CpuSparseMla
-    from tests.sparse_helpers import host_view
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        limit, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if limit != "max":
+            quota = int(limit) / int(period)
+    except (OSError, ValueError):
+        pass
+    threads = affinity if quota is None else max(1, min(affinity, math.ceil(quota)))
+    return threads, affinity, quota
 
-    inputs = result["_inputs"]
-    policy = inputs.policy
-    threads = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(threads)
-    rng = np.random.default_rng(0)
-    tokens = sorted(rng.choice(policy["T"], min(sample_tokens, policy["T"]), replace=False).tolist())
-    data = host_view(inputs, tokens)
-    q_rows = np.stack([data["q"][t] for t in tokens])
-    ref = CpuSparseMla(data, policy, q_rows, tokens)
-    ref.run()  # warm
-    runs = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        ref.run()
-        runs.append(time.perf_counter() - t0)
-    seconds = statistics.median(runs)
-    fraction = len(tokens) / policy["T"]
-    flops = result["flops"] * fraction
-    cpu_model = "unknown"
+
+def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return "unknown"
+
+
+def median_seconds(fn, repeats):
+    fn()  # warm
+    runs = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        runs.append(time.perf_counter() - t0)
+    return statistics.median(runs)
+
+
+def cpu_sparse(result, sample_tokens, seed=0):
+    """The oracle's vectorised FP32 PyTorch-CPU sparse MLA (the reference's
+    batched FP32 reference, sparse_reference.py:141-171) on a token sample of
+    one configuration; the rate is scaled to the whole configuration."""
+    import numpy as np
+
+    from oracle.cpu_reference import CpuSparseMla, host_view
+
+    inputs = result["_inputs"]
+    policy = inputs.policy
+    t = policy["T"]
+    rng = np.random.default_rng(seed)
+    tokens = list(range(t)) if sample_tokens >= t else sorted(rng.choice(t, sample_tokens, replace=False).tolist())
+    data = host_view(inputs, tokens)
+    ref = CpuSparseMla(data, policy, np.stack([data["q"][k] for k in tokens]), tokens)
+    seconds = median_seconds(ref.run, 3)
+    fraction = len(tokens) / t
     return {
-        "value": round(flops / seconds / 1e12, 4),
-        "unit": "TFLOPS",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{len(tokens)} of {policy['T']} tokens of {result['workload']}; median of 3 runs "
-                  f"{seconds:.3f} s (scaled full config {seconds / fraction * 1e3:.1f} ms); "
-                  f"FP32 torch CPU, {cpu_model}",
         "ms_full_scaled": round(seconds / fraction * 1e3, 2),
+        "tflops": round(result["flops"] * fraction / seconds / 1e12, 4),
+        "sample": f"{len(tokens)} of {t} tokens of {result['workload']}, median of 3 runs {seconds:.3f} s"
+                  + ("" if fraction == 1 else f", scaled by {t}/{len(tokens)}"),
+    }
+
+
+def cpu_flash_c2(heads=2):
+    """FP32 PyTorch-CPU softmax attention for FA C2 (B1 H32 S8192 D128, the
+    reference's FP32 attention math) on ``heads`` whole heads, in 1024-query
+    blocks; the rate is scaled to all 32 heads."""
+    import torch
+
+    gen = torch.Generator()
+    gen.manual_seed(9102201)
+    q, k, v = (torch.randn((heads, 8192, 128), generator=gen).half().float() for _ in range(3))
+    scale = 128 ** -0.5
+
+    @torch.inference_mode()
+    def run():
+        out = torch.empty_like(q)
+        for h in range(heads):
+            kt = k[h].t().contiguous()
+            for first in range(0, 8192, 1024):
+                scores = (q[h, first : first + 1024] @ kt) * scale
+                out[h, first : first + 1024] = torch.softmax(scores, dim=-1) @ v[h]
+        return out
+
+    seconds = median_seconds(run, 3)
+    flops = 4 * heads * 128 * 8192 * 8192
+    return {
+        "ms_full_scaled": round(seconds * 32 / heads * 1e3, 2),
+        "tflops": round(flops / seconds / 1e12, 4),
+        "sample": f"{heads} of 32 heads of FA B1 H32 S8192 D128 non-causal, median of 3 runs {seconds:.3f} s, "
+                  f"scaled by 32/{heads}",
     }
 
 
@@ -223,7 +271,8 @@ def main():
     parser.add_argument("--no-attention", action="store_true", help="skip the flash/teaching attention extras")
     parser.add_argument("--prewarm", type=float, default=1.0,
                         help="seconds of untimed launches before the first timed configuration (clock ramp)")
-    parser.add_argument("--cpu-sample", type=int, default=1024, help="tokens in the CPU-baseline sample")
+    parser.add_argument("--cpu-sample", type=int, default=2048,
+                        help="tokens in the CPU-baseline sample of each prefill configuration")
     parser.add_argument("--no-flush", action="store_true", help="keep caches warm between launches")
     parser.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                         help="also run a plain device copy of MIB MiB (PMC byte-counter calibration)")
@@ -269,26 +318,42 @@ def main():
         "decode768": ("sparse_mla decode B128x6 ctx131072", 128, 6, 131072),
     }
     order = [args.only] if args.only else ["prefill8k", "decode", "prefill32k", "decode768"]
-    results = {}
+    # CPU-baseline samples per configuration (tokens): about a second of CPU work each.
+    cpu_samples = {"prefill8k": args.cpu_sample, "decode": 384, "prefill32k": args.cpu_sample, "decode768": 768}
+    threads, affinity, quota = cpu_threads()
+    torch.set_num_threads(threads)
+    results, cpu = {}, {}
     for key in order:
         name, b, q, ctx = configs[key]
         results[key] = sparse_config(name, b, q, ctx, args.steps, args.warmup, flush, device,
                                      prewarm=args.prewarm if key == order[0] else 0.0)
-        if key != order[0]:
-            results[key].pop("_inputs")  # free device memory of secondary configs
-            torch.cuda.empty_cache()
+        if not args.no_cpu_baseline:
+            log(f"[bench] timing the CPU baseline of {key}")
+            cpu[key] = cpu_sparse(results[key], cpu_samples[key])
+            log(f"[bench] CPU {key}: {cpu[key]['ms_full_scaled']} ms (scaled), {cpu[key]['tflops']} TFLOPS")
+        results[key].pop("_inputs")  # free device memory before the next configuration
+        torch.cuda.empty_cache()
 
     extras = {}
     if not args.only and not args.no_attention:
         extras = attention_extras(args.steps, args.warmup, flush, device)
+        if not args.no_cpu_baseline:
+            cpu["fa_c2"] = cpu_flash_c2()
+            log(f"[bench] CPU fa_c2: {cpu['fa_c2']['ms_full_scaled']} ms (scaled)")
 
     head_key = order[0]
     head = results[head_key]
     baseline = None
-    if not args.no_cpu_baseline:
-        log("[bench] timing CPU baseline")
-        baseline = cpu_baseline(head, args.cpu_sample)
-    head.pop("_inputs", None)
+    host = f"FP32 torch CPU, {threads} threads ({affinity} CPUs in the affinity mask" + (
+        f", cgroup quota {quota:g} CPUs)" if quota is not None else ", no cgroup quota)") + f", {cpu_model()}"
+    if head_key in cpu:
+        baseline = {
+            "value": cpu[head_key]["tflops"],
+            "unit": "TFLOPS",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"{cpu[head_key]['sample']}; {host}",
+        }
 
     bound = "hbm" if head_key == "decode" else "mfma"
     achieved = head["gbs"] if bound == "hbm" else head["tflops"]
@@ -320,13 +385,13 @@ def main():
             "frac": round(achieved / peak, 4),
             "traffic": profiled_traffic(head_key),
         },
-        "cpu_baseline": {k: v for k, v in baseline.items() if k != "ms_full_scaled"} if baseline else None,
+        "cpu_baseline": baseline,
         "extra": {k: {kk: vv for kk, vv in v.items() if kk != "_inputs"} for k, v in results.items()},
         "reference_ascend_910b3_ms": {"prefill8k": 6.847, "prefill32k": 27.225, "decode": 0.410, "decode768": 0.810},
     }
     record["extra"].update(extras)
-    if baseline:
-        record["extra"]["cpu_ms_full_scaled"] = baseline["ms_full_scaled"]
+    if cpu:
+        record["extra"]["cpu_baseline_per_config"] = dict(cpu, host=host)
     print(json.dumps(record), flush=True)
     return 0
 

@@ -59,10 +59,15 @@ typedef struct SparseMlaParams {
    * deterministic for a given value. No counterpart in the reference, whose
    * sizes are compile-time constants. */
   int32_t parts;
-  /* Optional debug image of the row selection, NULL normally: int32 [T, S, 2]
-   * holding (cache, physical_row) per gather slot, cache 0 = ori_kv,
-   * 1 = cmp_kv, (-1, -1) for an unused slot.  Written by the fused kernel
-   * itself, from the same row list it then attends over. */
+  /* Optional debug image of the row selection, NULL normally: int32 [T, S, 2].
+   * Entry r < n of token t is the r-th row of the compacted row list the
+   * attention kernel streams for t (the LDS list it attends over, copied out
+   * after it is built), as (cache, physical_row), cache 0 = ori_kv,
+   * 1 = cmp_kv, in slot order (window positions, then compressed ranks,
+   * duplicates kept); entries from n on are (-1, -1). A call with it set
+   * resolves rows inside the attention kernel and splits no key. The
+   * per-slot layout of the reference's gather workspace is
+   * launch_sparse_mla_gather's. */
   int32_t* debug_rows;
   /* Optional f32 [T, H] output, NULL normally: the natural-log softmax
    * normaliser ln(sum_j e^(s_j) + e^sink[h]) of each (token, head), s_j =
@@ -85,7 +90,12 @@ typedef struct SparseMlaParams {
  * memory that the call may overwrite. With a workspace and at least two work
  * items (token x BM-head tile) per compute unit, a plan kernel first writes
  * every token's selected-row list into it and a persistent attention kernel
- * streams the items of each compute unit over those lists; otherwise (or with
+ * streams the items of each compute unit over those lists. The plan is:
+ * int32 counts [T] at byte 0 (selected rows per token), then, from byte
+ * round_up(4 T, 256), uint32 lists [T][round_up(WINDOW + TOPK, 256)] of
+ * tagged rows (bit 31 set: cmp_kv row, else ori_kv row; physical row in the
+ * low bits) in slot order, padded with the token's first row to a multiple of
+ * 32 entries (32 entries of ori_kv row 0 for an empty selection); otherwise (or with
  * params->debug_rows set) one workgroup per item (or per part of a split key,
  * params->parts, whose records a merge kernel then combines in the workspace)
  * resolves its rows itself. With one part, results are bit-identical either

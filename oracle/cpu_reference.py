@@ -16,7 +16,31 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .sparse_reference import PatchedRows, selected_physical
+from .sparse_reference import CMP_BIT, PatchedRows, selection_tagged
+
+# Integer metadata of a sparse call, in the reference entry order.
+INT_KEYS = ("cmp_sparse_indices", "ori_block_table", "cmp_block_table", "cu_seqlens_q", "seqused_ori_kv",
+            "seqused_cmp_kv", "cmp_residual_kv", "ori_topk_length")
+
+
+def host_view(inputs, tokens):
+    """Oracle data dict of device-built measurement inputs (an object with
+    ``policy``, ``host`` int32 metadata, device ``tensors`` and the ``touched``
+    rows of each cache): the metadata, the caches as ``PatchedRows`` of their
+    touched rows, and the queries of ``tokens`` only (a dict keyed by token)."""
+    d = inputs.policy["D"]
+    data = {k: inputs.host[k] for k in INT_KEYS}
+    data["sinks"] = inputs.tensors["sinks"].float().cpu().numpy()
+    for name in ("ori_kv", "cmp_kv"):
+        ids = inputs.touched[name]
+        flat = inputs.tensors[name].view(-1, d)
+        values = (flat[torch.from_numpy(ids).to(flat.device)].float().cpu().numpy() if len(ids)
+                  else np.zeros((0, d), np.float32))
+        data[name] = PatchedRows(ids, values)
+    index = torch.as_tensor(list(tokens), device=inputs.tensors["q"].device, dtype=torch.long)
+    rows = inputs.tensors["q"][index].float().cpu().numpy()
+    data["q"] = {token: rows[i] for i, token in enumerate(tokens)}
+    return data
 
 
 class CpuSparseMla:
@@ -39,14 +63,21 @@ class CpuSparseMla:
             tables.append((ids, values))
         zero_row = sum(len(v) for _, v in tables)
         self.rows = torch.from_numpy(np.concatenate([v for _, v in tables] + [np.zeros((1, d), np.float32)]))
+        # Selected rows are compacted in slot order (window positions, then the
+        # valid compressed ranks): the softmax over a set of rows does not
+        # depend on where in the gather workspace each one sits.
         index = np.full((len(self.tokens), s), zero_row, np.int64)
         valid = np.zeros((len(self.tokens), s), bool)
         for i, token in enumerate(self.tokens):
-            for slot, cache, row in selected_physical(data, policy, token):
+            tagged = selection_tagged(data, policy, token)
+            for cache in (0, 1):
+                which = np.flatnonzero((tagged >> 31) == cache)
+                rows = (tagged[which] & (CMP_BIT - 1)).astype(np.int64)
                 ids = tables[cache][0]
-                at = int(np.searchsorted(ids, row))
-                index[i, slot] = offsets[cache] + at if at < len(ids) and ids[at] == row else zero_row
-                valid[i, slot] = True
+                at = np.minimum(np.searchsorted(ids, rows), max(len(ids) - 1, 0))
+                hit = (ids[at] == rows) if len(ids) else np.zeros(len(rows), bool)
+                index[i, which] = np.where(hit, offsets[cache] + at, zero_row)
+            valid[i, : len(tagged)] = True
         self.index = torch.from_numpy(index)
         self.valid = torch.from_numpy(valid)
         self.q = torch.from_numpy(np.ascontiguousarray(q_rows, np.float32))

@@ -130,6 +130,26 @@ def selected_physical(data, policy, token):
     return out
 
 
+CMP_BIT = 1 << 31  # tag of a cmp_kv row in a tagged row id
+
+
+def selection_tagged(data, policy, token):
+    """``selected_physical`` of one token as tagged uint32 row ids in slot order
+    (bit 31 set for a cmp_kv row), vectorised with NumPy: the same geometry
+    and the same per-rank rule. Pinned against ``selected_physical`` on every
+    validation case."""
+    page = policy["PAGE"]
+    cpage = page // policy["RATIO"]
+    batch, right, visible, available, cutoff = query_geometry(data, policy, token)
+    positions = np.arange(right - visible, right, dtype=np.int64)
+    window = np.asarray(data["ori_block_table"])[batch, positions // page].astype(np.int64) * page + positions % page
+    bound = min(policy["TOPK"], available, cutoff)
+    index = np.asarray(data["cmp_sparse_indices"])[token, 0, : max(bound, 0)].astype(np.int64)
+    index = index[(index >= 0) & (index < cutoff)]
+    compressed = np.asarray(data["cmp_block_table"])[batch, index // cpage].astype(np.int64) * cpage + index % cpage
+    return np.concatenate([window, compressed | CMP_BIT]).astype(np.uint32)
+
+
 class PatchedRows:
     """A cache that is zero except for listed rows (the measurement caches).
 

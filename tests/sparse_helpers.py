@@ -7,11 +7,10 @@ import numpy as np
 import torch
 
 from oracle import sparse_reference as sr
+from oracle.cpu_reference import INT_KEYS, host_view  # noqa: F401  (re-exported for the tests)
 from oracle.dtypes import rounded
 
 TORCH_DTYPE = {"bf16": torch.bfloat16, "f16": torch.float16}
-INT_KEYS = ("cmp_sparse_indices", "ori_block_table", "cmp_block_table", "cu_seqlens_q", "seqused_ori_kv",
-            "seqused_cmp_kv", "cmp_residual_kv", "ori_topk_length")
 GUARD_WORDS = 256  # 512 guard bytes after the output (benchmarks/attention/run_sparse.py:31)
 
 
@@ -44,30 +43,61 @@ def guard_intact(tensors):
     return bool(torch.isnan(tail.float()).all())
 
 
-def host_view(inputs, tokens):
-    """Oracle data dict for device-built ``SparseInputs``: metadata, patched caches,
-    queries of ``tokens`` only (a dict keyed by token)."""
-    policy, d = inputs.policy, inputs.policy["D"]
-    data = {k: inputs.host[k] for k in INT_KEYS}
-    data["sinks"] = inputs.tensors["sinks"].float().cpu().numpy()
-    for name in ("ori_kv", "cmp_kv"):
-        ids = inputs.touched[name]
-        flat = inputs.tensors[name].view(-1, d)
-        values = flat[torch.from_numpy(ids).to(flat.device)].float().cpu().numpy() if len(ids) else np.zeros((0, d), np.float32)
-        data[name] = sr.PatchedRows(ids, values)
-    index = torch.as_tensor(list(tokens), device=inputs.tensors["q"].device, dtype=torch.long)
-    rows = inputs.tensors["q"][index].float().cpu().numpy()
-    data["q"] = {token: rows[i] for i, token in enumerate(tokens)}
-    return data
+CMP_BIT = sr.CMP_BIT  # row-list tag of a cmp_kv row
+CHUNK = 32            # rows per streamed chunk
+selection_tagged = sr.selection_tagged
 
 
 def expected_rows(data, policy, tokens):
-    """Oracle selection as the kernel's debug image: int32 [n, S, 2]."""
+    """Oracle selection as the kernel's debug image: int32 [n, S, 2], entry r
+    the r-th selected row (cache, physical row) in slot order, then (-1, -1)."""
     img = np.full((len(tokens), policy["S"], 2), -1, np.int32)
     for i, token in enumerate(tokens):
-        for slot, cache, row in sr.selected_physical(data, policy, token):
-            img[i, slot] = (cache, row)
+        tagged = selection_tagged(data, policy, token)
+        img[i, : len(tagged), 0] = (tagged >> 31).astype(np.int32)
+        img[i, : len(tagged), 1] = (tagged & (CMP_BIT - 1)).astype(np.int32)
     return img
+
+
+def expected_plan(data, policy, tokens):
+    """Oracle selection as the plan workspace holds it: counts [n] and the
+    tagged lists, padded with the first row to whole chunks ([CHUNK] zeros
+    for an empty selection), as a list of uint32 arrays."""
+    counts, lists = [], []
+    for token in tokens:
+        tagged = selection_tagged(data, policy, token)
+        counts.append(len(tagged))
+        if len(tagged):
+            padded = -(-len(tagged) // CHUNK) * CHUNK
+            lists.append(np.concatenate([tagged, np.full(padded - len(tagged), tagged[0], np.uint32)]))
+        else:
+            lists.append(np.zeros(CHUNK, np.uint32))
+    return np.array(counts, np.int32), lists
+
+
+def plan_from_workspace(workspace, policy):
+    """Counts [T] and the full list table [T, entries] (uint32) read back from a workspace."""
+    from ascendflow_amd.sparse_attention.attention import plan_layout
+
+    t = policy["T"]
+    count_at, rows_at, entries = plan_layout(t, policy["WINDOW"], policy["TOPK"])
+    raw = workspace.cpu().numpy()
+    counts = raw[count_at : count_at + 4 * t].view(np.int32)
+    table = raw[rows_at : rows_at + 4 * t * entries].view(np.uint32).reshape(t, entries)
+    return counts, table
+
+
+def assert_plan_matches(workspace, data, policy, tokens):
+    """Bit-exact: the plan the persistent kernel streamed equals the oracle's
+    selection, compacted and padded, for every token in ``tokens``."""
+    counts, table = plan_from_workspace(workspace, policy)
+    want_counts, want_lists = expected_plan(data, policy, tokens)
+    np.testing.assert_array_equal(counts[list(tokens)], want_counts)
+    for token, want in zip(tokens, want_lists):
+        got = table[token, : len(want)]
+        if not np.array_equal(got, want):
+            bad = int(np.flatnonzero(got != want)[0])
+            raise AssertionError(f"plan list of token {token} differs at entry {bad}: {got[bad]:#x} != {want[bad]:#x}")
 
 
 def assert_close(actual, ref_fp32, dtype):

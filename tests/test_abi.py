@@ -39,7 +39,19 @@ def test_kernel_config_and_workspace_queries(lib):
         has_workspace = kernel == "sparse_mla"
         assert cfg[0] == tensors and cfg[2] == int(has_workspace) and cfg[3] == 256 and cfg[4] == 4
         meta = json.loads(getattr(lib, f"kernel_metadata_{kernel}")().decode())
-        assert meta["kernel"] == kernel and len(meta["tensors"]) == tensors
+        # The reference's schema (src/backend/abi.py:19-59, consumed by
+        # src/runtime/torch.py:94-167): name, target, tensors with dtype,
+        # shape, layout and access, parameters with minimum and multiple.
+        assert meta["version"] == 1 and meta["name"] == kernel and meta["target"] == "gfx950"
+        assert len(meta["tensors"]) == tensors
+        for spec in meta["tensors"]:
+            assert set(spec) == {"name", "dtype", "shape", "layout", "access"}
+            assert spec["layout"] == "linear" and spec["access"] in ("read", "write")
+            assert all(isinstance(n, (int, str)) for n in spec["shape"])
+            assert spec["dtype"] in ("bf16", "f16", "f32", "i32") or spec["dtype"] in meta.get("dtypes", {})
+        for spec in meta["parameters"]:
+            assert set(spec) == {"name", "minimum", "multiple"} and spec["minimum"] >= 1 and spec["multiple"] >= 1
+            assert any(spec["name"] in t["shape"] for t in meta["tensors"])
         assert meta["disjoint_external"] is True and meta["workspace"] is has_workspace
     size = ct.c_uint64(123)
     # The sparse workspace is the row-list plan: T counts rounded up to 256
@@ -76,6 +88,7 @@ def test_kernel_config_and_workspace_queries(lib):
     assert size.value == 2048 + 512 * 768 * 4 + 512 * 3 * per_part
     for parts in (-1, 9):
         assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(good_params(parts=parts))) == -2
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(good_params(WINDOW=0, TOPK=0, S=0))) == -2
     assert lib.workspace_size_sparse_mla(ct.byref(size), None) == -1
     assert lib.workspace_size_sparse_mla(None, None) == -1
     assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(good_params(D=64))) == -2
@@ -110,6 +123,8 @@ def good_params(**overrides):
         ({"scale": 0.0}, -2),
         ({"dtype": 7}, -3),
         ({"ORI_BLOCKS": 1 << 24}, -2),
+        # No gather slot at all: nothing to stream (the row lists would be empty).
+        ({"WINDOW": 0, "TOPK": 0, "S": 0}, -2),
     ],
 )
 def test_sparse_launcher_rejects_bad_configurations_before_any_launch(lib, overrides, status):

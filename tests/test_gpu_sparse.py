@@ -1,11 +1,14 @@
 """GPU parity of the fused sparse-MLA kernel against the CPU oracle.
 
-Row selection is checked bit-exactly through the kernel's own debug image of
-its row list and through the gather-image kernel; outputs against the FP32
-oracle under the tolerance contract (max|err| <= 1e-2 * max|ref|, plus the
-reference runner's rtol 0.02 / atol 0.005). Every case also checks the 512
-guard bytes after the output and that no input changed
-(benchmarks/attention/run_sparse.py:241-262 does the same on Ascend).
+Row selection is checked bit-exactly on the lists the kernels stream: the
+plan workspace the persistent kernel reads (read back after the call), and
+the one-item kernel's LDS row list (copied out through the debug image), plus
+the per-slot gather image (the layout of the reference's gather workspace,
+benchmarks/attention/run_sparse.py:111-130,253-262). Outputs are checked
+against the FP32 oracle under the tolerance contract (max|err| <= 1e-2 *
+max|ref|, plus the reference runner's rtol 0.02 / atol 0.005). Every case also
+checks the 512 guard bytes after the output and that no input changed
+(run_sparse.py:241-262 does the same on Ascend).
 """
 
 import numpy as np
@@ -13,8 +16,8 @@ import pytest
 import torch
 
 from oracle import sparse_reference as sr
-from tests.sparse_helpers import (INT_KEYS, assert_close, call_args, call_kwargs, expected_rows, guard_intact, host_view,
-                                  to_device)
+from tests.sparse_helpers import (INT_KEYS, assert_close, assert_plan_matches, call_args, call_kwargs, expected_rows,
+                                  guard_intact, host_view, to_device)
 
 pytestmark = pytest.mark.gpu
 
@@ -104,7 +107,25 @@ def test_validation_cases_match_oracle(device, case, variant):
             assert np.all(split == 0), f"empty selection not zero with parts={parts}"
 
 
-@pytest.mark.parametrize("variant", [v for v in VARIANTS if "topk" not in v])
+PERSISTENT_VARIANTS = dict({v: VARIANTS[v] for v in VARIANTS if "topk" not in v},
+                           # WINDOW + TOPK = 3712 slots: the plan kernel resolves a token in six
+                           # sequences of round trips, and the persistent kernel's list ring holds
+                           # 3840-entry lists (D = 256 leaves room for them next to the KV ring).
+                           **{"bf16-d256-bm64-r2-topk3584": dict(DTYPE="bf16", D=256, H=64, BM=64, RATIO=2, TOPK=3584,
+                                                                 MAX_SEQ=16384)})
+
+
+def workspace_for(policy, device, parts=None):
+    """A caller workspace for one call, filled with a sentinel so a plan the
+    kernel did not write cannot pass for one."""
+    from ascendflow_amd.sparse_attention.attention import workspace_bytes
+
+    kw = {k: policy[k] for k in ("B", "T", "H", "D", "PAGE", "RATIO", "MAX_SEQ", "ORI_BLOCKS", "CMP_BLOCKS", "WINDOW",
+                                 "TOPK", "S", "BM", "DTYPE", "SCALE")}
+    return torch.full((workspace_bytes(**kw, parts=parts),), 0xCD, dtype=torch.uint8, device=device)
+
+
+@pytest.mark.parametrize("variant", list(PERSISTENT_VARIANTS))
 def test_persistent_stream_matches_fused_and_oracle(device, variant):
     """T = 544 tokens: at least two work items per CU, so the plan path runs
     the persistent kernel, whose workgroups stream many tokens (and, with
@@ -115,7 +136,9 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
     selections (the split runs on the one-item kernel, then the merge)."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
-    policy = sr.default_policy(B=6, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
+    print(f"\n[sparse] persistent stream variant={variant}", flush=True)
+    policy = sr.default_policy(**dict(dict(B=6, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160),
+                                      **PERSISTENT_VARIANTS[variant]))
     data = sr.inputs(policy, "mixed")
     tensors = to_device(data, policy, device)
     debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
@@ -125,11 +148,15 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
     fused, fused_lse = tensors["attention_out"].clone(), lse.clone()
     tensors["attention_out"].fill_(float("nan"))
     lse.fill_(float("nan"))
-    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse)
+    workspace = workspace_for(policy, device, parts=1)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse, workspace=workspace)
     torch.cuda.synchronize()
     assert guard_intact(tensors), "kernel wrote past attention_out"
     assert torch.equal(fused, tensors["attention_out"]), "persistent stream differs from the in-kernel row resolution"
     assert torch.equal(fused_lse, lse), "persistent softmax_lse differs from the in-kernel row resolution"
+    every = list(range(policy["T"]))
+    assert_plan_matches(workspace, data, policy, every)
+    np.testing.assert_array_equal(debug.cpu().numpy(), expected_rows(data, policy, every))
     rows = (debug[..., 0] >= 0).sum(dim=1).cpu().numpy()
     rng = np.random.default_rng(11)
     tokens = sorted({0, 1, 543, *np.flatnonzero(rows <= 1)[:8].tolist(), *rng.choice(544, 24, replace=False).tolist()})
@@ -150,6 +177,55 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
         assert_lse(lse[index], lse_ref)
 
 
+@pytest.mark.parametrize("variant", ["bf16-d512-bm64-r2", "f16-d256-bm64-r1"])
+@pytest.mark.parametrize("case", sr.CASES)
+def test_validation_cases_on_the_persistent_stream(device, case, variant):
+    """The eight validation cases (sparse_reference.py:45-104) at B8 x T544,
+    i.e. more than two work items per CU, so the plain call takes the plan
+    kernel + persistent kernel: empty selections, a ragged batch with an empty
+    request, replay narrowing, padding, duplicates and sinks of +-80 all run
+    through one continuous chunk stream per CU. The plan it streamed must equal
+    the oracle's selection for every token, its output and softmax_lse must be
+    bit-identical to the one-item kernel (whose own row list is checked through
+    the debug image) and match the oracle on a sample."""
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    print(f"\n[sparse] persistent case={case} variant={variant}", flush=True)
+    policy = sr.default_policy(B=8, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
+    policy["SCALE"] = policy["D"] ** -0.5
+    data = sr.inputs(policy, case)
+    tensors = to_device(data, policy, device)
+    before = {k: tensors[k].clone() for k in sr.TENSOR_ORDER if k != "attention_out"}
+    t = policy["T"]
+    debug = torch.full((t, policy["S"], 2), -7, dtype=torch.int32, device=device)
+    lse_one = torch.full((t, policy["H"]), float("nan"), dtype=torch.float32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug, softmax_lse=lse_one)
+    torch.cuda.synchronize()
+    one_item = tensors["attention_out"].clone()
+    tensors["attention_out"].fill_(float("nan"))
+    lse = torch.full_like(lse_one, float("nan"))
+    workspace = workspace_for(policy, device, parts=1)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse, workspace=workspace)
+    torch.cuda.synchronize()
+    assert guard_intact(tensors), "kernel wrote past attention_out"
+    for k, v in before.items():
+        assert torch.equal(tensors[k], v), f"input {k} changed"
+    every = list(range(t))
+    assert_plan_matches(workspace, data, policy, every)
+    np.testing.assert_array_equal(debug.cpu().numpy(), expected_rows(data, policy, every))
+    assert torch.equal(one_item, tensors["attention_out"]), "persistent stream differs from the one-item kernel"
+    assert torch.equal(lse_one, lse), "persistent softmax_lse differs from the one-item kernel"
+    out = tensors["attention_out"].float().cpu().numpy()
+    if case == "empty":
+        assert np.all(out == 0)
+    counts = (debug[..., 0] >= 0).sum(dim=1).cpu().numpy()
+    rng = np.random.default_rng(3)
+    tokens = sorted({0, 1, t - 1, *np.flatnonzero(counts <= 1)[:6].tolist(), *np.flatnonzero(counts == counts.max())[:2].tolist(),
+                     *rng.choice(t, 24, replace=False).tolist()})
+    assert_close(out[tokens], sr.oracle_fp32(data, policy, tokens), policy["DTYPE"])
+    assert_lse(lse[torch.as_tensor(tokens, device=device)], sr.oracle_lse(data, policy, tokens))
+
+
 def test_relaunch_is_bitwise_deterministic(device):
     from ascendflow_amd.sparse_attention import sparse_mla
 
@@ -164,26 +240,43 @@ def test_relaunch_is_bitwise_deterministic(device):
     assert torch.equal(first, tensors["attention_out"])
 
 
-def check_measured(inputs, tokens, device, split=False):
+def metadata_view(inputs):
+    """The integer metadata of device-built inputs as an oracle data dict (no rows)."""
+    return {k: inputs.host[k] for k in INT_KEYS}
+
+
+def check_measured(inputs, tokens, device, split=False, plan=False):
     """Runs without the debug image first (the path the benchmark takes), then
     with it (in-kernel row resolution, one part per token). Unless the plan
     path splits tokens into parts (``split``: the merge sums in another
     order), the debug dump must not change any output bit; both outputs must
-    match the oracle, and the debug image the oracle's selection."""
+    match the oracle on ``tokens``. The debug image (the one-item kernel's
+    streamed row list) must equal the oracle's selection for every token; with
+    ``plan`` the plain call ran the plan + persistent path, and the plan it
+    streamed (read back from the workspace) must too."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
     policy = inputs.policy
-    sparse_mla(*inputs.call_args(), **inputs.call_kwargs())
+    workspace = workspace_for(policy, device)
+    sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), workspace=workspace)
     torch.cuda.synchronize()
     plain = inputs.tensors["attention_out"].clone()
+    every = list(range(policy["T"]))
+    meta = metadata_view(inputs)
+    if plan:
+        assert_plan_matches(workspace, meta, policy, every)
+    del workspace
     debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
     sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), debug_rows=debug)
     torch.cuda.synchronize()
     if not split:
         assert torch.equal(plain, inputs.tensors["attention_out"]), "the debug image changed the output"
+    for first in range(0, policy["T"], 4096):
+        part = every[first : first + 4096]
+        np.testing.assert_array_equal(debug[first : first + len(part)].cpu().numpy(), expected_rows(meta, policy, part))
+    del debug
     data = host_view(inputs, tokens)
     index = torch.as_tensor(tokens, device=device)
-    np.testing.assert_array_equal(debug[index].cpu().numpy(), expected_rows(data, policy, tokens))
     ref = sr.oracle_fp32(data, policy, tokens)
     assert_close(plain[index].float().cpu().numpy(), ref, policy["DTYPE"])
     actual = inputs.tensors["attention_out"][index].float().cpu().numpy()
@@ -249,7 +342,26 @@ def test_prefill_q8k_ctx32k_sampled_tokens(device):
     inputs = make_inputs(policy, 32768, device=device)
     rng = np.random.default_rng(5)
     tokens = sorted({0, 1, 31, 32, 8191, *rng.choice(8192, 90, replace=False).tolist()})
-    check_measured(inputs, tokens, device)
+    check_measured(inputs, tokens, device, plan=True)
+
+
+def test_prefill_q32k_ctx32k_all_rows_and_sampled_tokens(device):
+    """Prefill at scale (README.md:34): B1, Q 32768 tokens
+    over a 32K context, so selections grow from 1 row (token 0) to 640. The
+    plan + persistent path streams 128 work items per CU over a 100 MB plan:
+    its lists must equal the oracle's selection for all 32768 tokens, its
+    output must be bit-identical to the one-item kernel's (whose row lists
+    are checked for every token through the debug image) and match the FP32
+    oracle on spread tokens, including both ends and chunk/half boundaries."""
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+
+    print("\n[sparse] prefill T32768 ctx 32768", flush=True)
+    policy = measurement_policy(batch=1, query_tokens=32768, context=32768)
+    inputs = make_inputs(policy, 32768, device=device)
+    rng = np.random.default_rng(32)
+    tokens = sorted({0, 1, 31, 32, 63, 64, 255, 256, 1023, 8191, 8192, 16383, 16384, 32766, 32767,
+                     *rng.choice(32768, 90, replace=False).tolist()})
+    check_measured(inputs, tokens, device, plan=True)
 
 
 def test_prefill_from_empty_cache_has_growing_selections(device):
@@ -260,7 +372,7 @@ def test_prefill_from_empty_cache_has_growing_selections(device):
     policy = measurement_policy(batch=1, query_tokens=4096, context=4096)
     inputs = make_inputs(policy, 4096, device=device)
     tokens = list(range(0, 40)) + list(range(100, 4096, 97)) + [4095]
-    check_measured(inputs, tokens, device)
+    check_measured(inputs, tokens, device, plan=True)
 
 
 def test_decode_b128x6_ctx128k_sampled_tokens(device):
@@ -273,7 +385,7 @@ def test_decode_b128x6_ctx128k_sampled_tokens(device):
     inputs = make_inputs(policy, 131072, device=device)
     rng = np.random.default_rng(7)
     tokens = sorted({0, 5, 6, 767, *rng.choice(768, 60, replace=False).tolist()})
-    check_measured(inputs, tokens, device)
+    check_measured(inputs, tokens, device, plan=True)
 
 
 @pytest.mark.parametrize("variant", ["bf16-d512-bm64-r2", "f16-d256-bm64-r1", "bf16-d128-bm32-r2"])

@@ -77,3 +77,37 @@ def test_simple_reference_is_row_stochastic_mix_of_values():
     k[:] = 0
     v = rng.standard_normal((2, 128, 128)).astype(np.float32)
     np.testing.assert_allclose(simple_reference(q, k, v), np.broadcast_to(v.mean(axis=1, keepdims=True), (2, 64, 128)), rtol=1e-5, atol=1e-6)
+
+
+def test_simple_reference_equals_dense_softmax_on_random_inputs():
+    """Random q, k, v: a transposed K, a missing or wrong 128^-0.5 scale or a
+    softmax over the wrong axis changes the output. dense_reference (einsum,
+    GQA broadcast) is itself pinned by the closed forms above."""
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((3, 96, 128)).astype(np.float32)
+    k = rng.standard_normal((3, 128, 128)).astype(np.float32)
+    v = rng.standard_normal((3, 128, 128)).astype(np.float32)
+    dense = dense_reference(q[None], k[None], v[None], scale=128**-0.5, causal=False)[0]
+    np.testing.assert_allclose(simple_reference(q, k, v), dense, rtol=1e-5, atol=1e-6)
+    for wrong in (1.0, 0.125, 128**-0.5 * 1.01):
+        assert not np.allclose(dense_reference(q[None], k[None], v[None], scale=wrong)[0], dense, rtol=1e-4, atol=1e-5)
+    assert not np.allclose(simple_reference(q, k.transpose(0, 2, 1).copy(), v), dense, rtol=1e-4, atol=1e-5)
+
+
+def test_simple_reference_matches_textbook_softmax_brute_force():
+    """Scalar float64 loops of O[i] = sum_j softmax_j(q_i . k_j / sqrt(128)) v_j on a tiny input."""
+    import math
+
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((1, 3, 128)).astype(np.float32)
+    k = rng.standard_normal((1, 128, 128)).astype(np.float32)
+    v = rng.standard_normal((1, 128, 128)).astype(np.float32)
+    expected = np.zeros((1, 3, 128))
+    for i in range(3):
+        scores = [sum(float(q[0, i, d]) * float(k[0, j, d]) for d in range(128)) / math.sqrt(128) for j in range(128)]
+        top = max(scores)
+        weights = [math.exp(s - top) for s in scores]
+        total = sum(weights)
+        for j in range(128):
+            expected[0, i] += weights[j] / total * v[0, j].astype(np.float64)
+    np.testing.assert_allclose(simple_reference(q, k, v), expected, rtol=1e-5, atol=1e-6)

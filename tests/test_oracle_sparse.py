@@ -255,3 +255,27 @@ def test_lse_rebuilds_the_oracle_output(case):
             continue
         weights = np.exp(q @ rows.astype(np.float64).T * policy["SCALE"] - lse[token][:, None])
         np.testing.assert_allclose(out[token], weights @ rows, rtol=2e-4, atol=2e-6)
+
+
+@pytest.mark.parametrize("ratio", [1, 2])
+@pytest.mark.parametrize("case", sr.CASES)
+def test_vectorised_selection_and_plan_images_match_the_oracle(case, ratio):
+    """The GPU tests' fast selection images (tests/sparse_helpers.py) equal the
+    oracle's per-slot selection: tagged rows in slot order, the debug image,
+    and the padded plan lists (first row repeated, or CHUNK zeros when empty)."""
+    from tests.sparse_helpers import CHUNK, CMP_BIT, expected_plan, expected_rows, selection_tagged
+
+    policy = sr.default_policy(B=4, T=16, MAX_SEQ=4096, ORI_BLOCKS=64, CMP_BLOCKS=64, RATIO=ratio)
+    data = sr.inputs(policy, case)
+    tokens = list(range(policy["T"]))
+    image = expected_rows(data, policy, tokens)
+    counts, lists = expected_plan(data, policy, tokens)
+    for token in tokens:
+        chosen = sr.selected_physical(data, policy, token)
+        tagged = [(CMP_BIT if cache else 0) | row for _, cache, row in chosen]
+        assert selection_tagged(data, policy, token).tolist() == tagged
+        assert counts[token] == len(chosen)
+        assert image[token, : len(chosen)].tolist() == [[cache, row] for _, cache, row in chosen]
+        assert (image[token, len(chosen):] == -1).all()
+        want = tagged + [tagged[0]] * (-len(tagged) % CHUNK) if tagged else [0] * CHUNK
+        assert lists[token].tolist() == want
