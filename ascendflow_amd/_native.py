@@ -14,6 +14,7 @@ LIB_NAME = "libascendflow_amd.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 AFA_DTYPE = {"bf16": 0, "f16": 1}
+SCRATCH_BYTES = 32 << 20  # AFA_SCRATCH_BYTES: the allocation-free entry's static workspace per GPU
 STATUS = {
     -1: "AFA_E_NULL: a required pointer is NULL",
     -2: "AFA_E_SHAPE: unsupported or inconsistent size",
@@ -24,6 +25,7 @@ STATUS = {
 # Every symbol include/ascendflow_amd.h declares.
 EXPORTS = (
     "launch_sparse_mla",
+    "launch_sparse_mla_noalloc",
     "launch_sparse_mla_gather",
     "launch_attention_target",
     "launch_simple_attention",
@@ -80,6 +82,7 @@ class FaParams(ct.Structure):
 _P = ct.c_void_p
 _SIGNATURES = {
     "launch_sparse_mla": ([_P] * 15 + [ct.POINTER(SparseMlaParams)], ct.c_int),
+    "launch_sparse_mla_noalloc": ([_P] * 14 + [ct.POINTER(SparseMlaParams)], ct.c_int),
     "launch_sparse_mla_gather": ([_P] * 13 + [ct.POINTER(SparseMlaParams)], ct.c_int),
     "launch_attention_target": (
         [_P] * 6 + [ct.c_int64, ct.c_int64, ct.POINTER(FaParams)],

@@ -34,6 +34,8 @@
 // K and V are the same gathered rows; each row is read from global memory
 // once per workgroup and from LDS once per score wave and once per output wave.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1582,6 +1584,60 @@ extern "C" int launch_sparse_mla(void* stream, const void* q, const void* ori_kv
   }
   hipStream_t s = (hipStream_t)stream;
   return params->dtype == AFA_DTYPE_BF16 ? dispatch_d<DT_BF16>(a, s) : dispatch_d<DT_F16>(a, s);
+}
+
+// Scratch of the allocation-free entry point: the workspace of one call (the
+// row-list plan and any split records) in a file-scope device array, so the
+// call needs no allocation. Each GPU holds its own copy until the process ends;
+// every call on a GPU reuses it, so calls that overlap on one GPU race. Nothing
+// in it has to start at zero: each call writes every count, list entry and
+// record it later reads.
+constexpr size_t SCRATCH_BYTES = size_t(32) << 20;
+static_assert(SCRATCH_BYTES == AFA_SCRATCH_BYTES, "the header states the scratch size");
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+// Device address of the current GPU's copy of `scratch`, resolved once per
+// device with hipGetSymbolAddress (the array's name is a host-side stand-in,
+// not a device address, and must never be passed to a kernel or a copy).
+static int scratch_address(void** out) {
+  constexpr int MAX_DEVICES = 64;
+  static std::atomic<void*> address[MAX_DEVICES];
+  static std::mutex resolve;
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return (int)e;
+  if (device < 0 || device >= MAX_DEVICES) return AFA_E_SHAPE;
+  void* p = address[device].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> guard(resolve);
+    p = address[device].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (p == nullptr) return (int)hipErrorInvalidSymbol;
+      address[device].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return AFA_OK;
+}
+
+extern "C" int launch_sparse_mla_noalloc(void* stream, const void* q, const void* ori_kv,
+                                         const void* cmp_kv, const int32_t* cmp_sparse_indices,
+                                         const int32_t* ori_block_table, const int32_t* cmp_block_table,
+                                         const int32_t* cu_seqlens_q, const int32_t* seqused_ori_kv,
+                                         const int32_t* seqused_cmp_kv, const int32_t* cmp_residual_kv,
+                                         const int32_t* ori_topk_length, const float* sinks,
+                                         void* attention_out, const SparseMlaParams* params) {
+  const int status = check_sparse(params);
+  if (status) return status;
+  if (plan_bytes(params) > SCRATCH_BYTES) return AFA_E_WORKSPACE;
+  void* workspace = nullptr;
+  const int resolved = scratch_address(&workspace);
+  if (resolved) return resolved;
+  return launch_sparse_mla(stream, q, ori_kv, cmp_kv, cmp_sparse_indices, ori_block_table, cmp_block_table,
+                           cu_seqlens_q, seqused_ori_kv, seqused_cmp_kv, cmp_residual_kv, ori_topk_length, sinks,
+                           attention_out, workspace, params);
 }
 
 extern "C" int launch_sparse_mla_gather(void* stream, const void* ori_kv, const void* cmp_kv,

@@ -108,6 +108,26 @@ int launch_sparse_mla(void* stream, const void* q, const void* ori_kv, const voi
                       const float* sinks, void* attention_out, void* workspace,
                       const SparseMlaParams* params);
 
+/* Allocation-free variant of launch_sparse_mla, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference, whose
+ * runtime owns a workspace arena per stream binding (src/runtime/kernel.py:39-49).
+ * Same arguments without `workspace`: the call's workspace (row-list plan and
+ * split records, workspace_size_sparse_mla bytes) lives in a static device
+ * array of 32 MiB per GPU (AFA_SCRATCH_BYTES), resolved once per device; it
+ * allocates nothing. Returns AFA_E_WORKSPACE, before any launch, when the
+ * call's workspace exceeds it (e.g. a 32K-token prefill: 100 MiB). Results are
+ * bit-identical to launch_sparse_mla with a workspace. All calls on one GPU
+ * share the array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller. */
+#define AFA_SCRATCH_BYTES (32u << 20)
+int launch_sparse_mla_noalloc(void* stream, const void* q, const void* ori_kv, const void* cmp_kv,
+                              const int32_t* cmp_sparse_indices, const int32_t* ori_block_table,
+                              const int32_t* cmp_block_table, const int32_t* cu_seqlens_q,
+                              const int32_t* seqused_ori_kv, const int32_t* seqused_cmp_kv,
+                              const int32_t* cmp_residual_kv, const int32_t* ori_topk_length,
+                              const float* sinks, void* attention_out, const SparseMlaParams* params);
+
 /* Gather image of the sparse selection, the layout of the reference's gather
  * workspace and of its gather oracle (benchmarks/attention/sparse_reference.py:174-181,
  * examples/sparse_attention/gather.py:86-131, window slots from gather.py:38-60):

@@ -189,3 +189,15 @@ def test_framework_op_is_registered_with_a_shape_only_fake():
     assert lse.shape == (t, h) and lse.dtype == torch.float32
     _, empty = torch.ops.ascendflow_amd.sparse_flash_mla(*args)
     assert empty.numel() == 0
+
+
+def test_noalloc_entry_rejects_workspaces_beyond_its_scratch(lib):
+    """A call whose workspace exceeds the 32 MiB static scratch is refused with
+    AFA_E_WORKSPACE before anything is launched (a 32K-token prefill needs 100 MiB)."""
+    big = good_params(B=1, T=32768, MAX_SEQ=32768, parts=1)
+    size = ct.c_uint64(0)
+    assert lib.workspace_size_sparse_mla(ct.byref(size), ct.byref(big)) == 0 and size.value > _native.SCRATCH_BYTES
+    args = [None] + [ct.c_void_p(16)] * 13
+    assert lib.launch_sparse_mla_noalloc(*args, ct.byref(big)) == -4
+    assert lib.launch_sparse_mla_noalloc(*args, ct.byref(good_params(D=64))) == -2
+    assert lib.launch_sparse_mla_noalloc(*args, None) == -1
