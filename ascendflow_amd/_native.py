@@ -27,6 +27,8 @@ EXPORTS = (
     "launch_sparse_mla",
     "launch_sparse_mla_noalloc",
     "launch_sparse_mla_gather",
+    "launch_sparse_mla_plan",
+    "launch_gather_probe",
     "launch_attention_target",
     "launch_simple_attention",
     "kernel_config_sparse_mla",
@@ -84,6 +86,11 @@ _SIGNATURES = {
     "launch_sparse_mla": ([_P] * 15 + [ct.POINTER(SparseMlaParams)], ct.c_int),
     "launch_sparse_mla_noalloc": ([_P] * 14 + [ct.POINTER(SparseMlaParams)], ct.c_int),
     "launch_sparse_mla_gather": ([_P] * 13 + [ct.POINTER(SparseMlaParams)], ct.c_int),
+    "launch_sparse_mla_plan": ([_P] * 10 + [ct.POINTER(SparseMlaParams)], ct.c_int),
+    "launch_gather_probe": (
+        [_P] * 4 + [ct.POINTER(SparseMlaParams), ct.c_int32, ct.c_int32, ct.c_int32, _P],
+        ct.c_int,
+    ),
     "launch_attention_target": (
         [_P] * 6 + [ct.c_int64, ct.c_int64, ct.POINTER(FaParams)],
         ct.c_int,

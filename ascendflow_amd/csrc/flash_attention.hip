@@ -47,15 +47,17 @@ struct FaArgs {
 // Online softmax (attention.py:73-139) in FP32 registers, exp2 domain: the
 // chunk max is taken on raw scores (the scale is positive) and the scale goes
 // into the exponent's FMA; the running max is raised, with O and l rescaled
-// by alpha = 2^(m - m'), whenever some query's max grows (FA_TAU = 0), so
-// P <= 1 and the key holding the running max gets P = 1 exactly, as in the
-// reference's recurrence. A lazily raised reference point (P up to 2^TAU)
-// rounds the dominant key's P to the storage dtype instead; with bf16 (8-bit
-// mantissa) and sharp scores that alone moved outputs by 2 ulps.
+// by alpha = 2^(m - m'), only when some query's max exceeds it by more than
+// fa_tau, so P <= 2^fa_tau; O / l is independent of the reference point. The
+// lazy reference point rounds the P of the key holding the running max to the
+// storage dtype, where the reference's recurrence has P = 1 exactly: a
+// relative error of at most 2^-12 in f16 (within its contract; eager rescaling
+// measured 5% slower on FA C2) but 2^-9 in bf16, which with sharp scores moved
+// outputs by 2 ulps, so bf16 raises the max whenever it grows (fa_tau = 0).
 // Masks (attention.py:96-110): keys >= Sk, and for causal attention key j is
 // visible to query i iff j <= i (top-left); they are applied only in chunks
 // that reach the tail or the diagonal.
-constexpr float FA_TAU = 0.0f;
+template <int DT> __device__ constexpr float fa_tau() { return DT == DT_F16 ? 8.0f : 0.0f; }
 constexpr int FA_NSTAGE = 3;
 // Progress-ordered wave priorities: a wave starts each chunk at priority 3
 // and steps down at half of QK, after QK and at half of PV, so of the two waves
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       } else if (f == QT + 1) {
         bool grow = false;
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) grow |= m_new[qt] > m_run[qt] + FA_TAU;
+        for (int qt = 0; qt < QT; ++qt) grow |= m_new[qt] > m_run[qt] + fa_tau<DT>();
         if (__ballot(grow) != 0ull) {
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {

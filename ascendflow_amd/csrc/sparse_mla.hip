@@ -1327,6 +1327,92 @@ __global__ __launch_bounds__(256) void sparse_gather_kernel(SparseArgs a, void* 
   }
 }
 
+// Gather probe, a measurement kernel with no counterpart on the attention path
+// (the reference's standalone gather micro-benchmark is
+// benchmarks/attention/gather_dma.py): streams the row lists of a plan
+// workspace through LDS the way the attention kernels move KV rows
+// (load-to-LDS, one wave load per 1 KiB row, the same XOR swizzle), in
+// 16-row chunks with DEPTH chunks in flight per workgroup, and no compute. It
+// measures the HBM rate the sparse access pattern itself reaches at a given
+// depth. Each workgroup takes up to PROBE_ITEMS items: items worker,
+// worker + G, ... (interleaved, as the persistent kernel), or, when balanced,
+// an equal range of the flat chunk stream of all items (every item streaming
+// as many chunks as item 0). One dword of every streamed row is read back from
+// LDS and summed per thread into sums[block][16], so the data can be checked.
+constexpr int PROBE_ROWS = 16;   // rows per probe chunk
+constexpr int PROBE_ITEMS = 4;   // most items one probe workgroup streams
+template <int DEPTH>
+__global__ __launch_bounds__(256) void gather_probe_kernel(const char* ori, const char* cmp, const int32_t* counts,
+                                                           const uint32_t* lists, int list_pad, int n_items,
+                                                           int balanced, uint32_t* sums) {
+  constexpr int NT = DEPTH + 1;  // ring tiles: the tile read at step s is never the one being filled
+  constexpr int ROW = 1024, PER_WAVE = PROBE_ROWS / 4;
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[NT][PROBE_ROWS * ROW];
+  extern __shared__ __attribute__((aligned(16))) uint32_t probe_lists[];  // [PROBE_ITEMS][list_pad]
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int G = (int)gridDim.x, worker = (int)xcd_contiguous(blockIdx.x, gridDim.x);
+  auto chunks_of = [&](int item) { const int n = counts[item]; return n > 0 ? (n + PROBE_ROWS - 1) / PROBE_ROWS : 1; };
+  // This workgroup's items and the chunk range of each.
+  int item[PROBE_ITEMS], first[PROBE_ITEMS], nch[PROBE_ITEMS], J = 0;
+  if (balanced) {
+    const int per = chunks_of(0);
+    const long total = (long)n_items * per;
+    const long f0 = total * worker / G, f1 = total * (worker + 1) / G;
+    for (long f = f0; f < f1 && J < PROBE_ITEMS;) {
+      const int it = (int)(f / per), c0 = (int)(f % per);
+      const int c1 = (int)min((long)per, f1 - (long)it * per);
+      item[J] = it; first[J] = c0; nch[J] = c1 - c0; ++J;
+      f = (long)it * per + c1;
+    }
+  } else {
+    for (int it = worker; it < n_items && J < PROBE_ITEMS; it += G) {
+      item[J] = it; first[J] = 0; nch[J] = chunks_of(it); ++J;
+    }
+  }
+  // Lists of all items to LDS, one round trip.
+  for (int j = 0; j < J; ++j)
+    for (int u = wave; u < list_pad / 256; u += 4)
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                       :: "s"(lds_address(probe_lists) + (uint32_t)(j * list_pad + u * 256) * 4u),
+                          "v"((uint32_t)lane * 16u), "s"(lists + (size_t)item[j] * list_pad + u * 256) : "memory");
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  block_barrier();
+  int total = 0, last[PROBE_ITEMS];
+  for (int j = 0; j < J; ++j) {
+    total += nch[j];
+    last[j] = chunks_of(item[j]) - 1;  // the plan holds whole chunks up to here
+  }
+  auto issue = [&](int s) {
+    int j = 0, c = s;
+    while (j + 1 < J && c >= nch[j]) c -= nch[j++];
+    // Balanced ranges assume item 0's chunk count for every item; an item
+    // with fewer listed chunks re-reads its last one, never unwritten entries.
+    c = min(c + first[j], last[j]);
+    const uint32_t tile = lds_address(tiles[s % NT]);
+#pragma unroll
+    for (int p = 0; p < PER_WAVE; ++p) {
+      const int r = wave * PER_WAVE + p;
+      const uint32_t e = __builtin_amdgcn_readfirstlane(probe_lists[j * list_pad + c * PROBE_ROWS + r]);
+      const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW;
+      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                       :: "s"(tile + (uint32_t)(r * ROW)), "v"((uint32_t)((lane ^ (r & 15)) << 4)), "s"(row) : "memory");
+    }
+  };
+  uint32_t acc = 0;
+  for (int s = 0; s < DEPTH && s < total; ++s) issue(s);
+  for (int s = 0; s < total; ++s) {
+    if (s + DEPTH - 1 < total)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((PER_WAVE * (DEPTH - 1)) & 15) | (((PER_WAVE * (DEPTH - 1)) >> 4) << 14));
+    else
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    block_barrier();
+    if (tid < PROBE_ROWS)  // unit 0 of row tid sits at position tid & 15
+      acc += *lds_at<uint32_t>(lds_address(tiles[s % NT]) + (uint32_t)(tid * ROW + ((tid & 15) << 4)));
+    if (s + DEPTH < total) issue(s + DEPTH);
+  }
+  if (tid < PROBE_ROWS) sums[(size_t)blockIdx.x * PROBE_ROWS + tid] = acc;
+}
+
 }  // namespace afa
 
 using namespace afa;
@@ -1667,6 +1753,59 @@ extern "C" int launch_sparse_mla_gather(void* stream, const void* ori_kv, const 
   else
     hipLaunchKernelGGL(sparse_gather_kernel<DT_F16>, dim3(params->T), dim3(256), 0, s, a, kv_out,
                        bias_out);
+  return (int)hipGetLastError();
+}
+
+// Plan only: the row-list plan of launch_sparse_mla's workspace (layout in
+// include/ascendflow_amd.h), written by the same plan kernel.
+extern "C" int launch_sparse_mla_plan(void* stream, const int32_t* cmp_sparse_indices,
+                                      const int32_t* ori_block_table, const int32_t* cmp_block_table,
+                                      const int32_t* cu_seqlens_q, const int32_t* seqused_ori_kv,
+                                      const int32_t* seqused_cmp_kv, const int32_t* cmp_residual_kv,
+                                      const int32_t* ori_topk_length, void* workspace,
+                                      const SparseMlaParams* params) {
+  const int status = check_sparse(params);
+  if (status) return status;
+  if (!cmp_sparse_indices || !ori_block_table || !cmp_block_table || !cu_seqlens_q || !seqused_ori_kv ||
+      !seqused_cmp_kv || !cmp_residual_kv || !ori_topk_length || !workspace)
+    return AFA_E_NULL;
+  SparseArgs a = make_args(params, nullptr, nullptr, nullptr, cmp_sparse_indices, ori_block_table, cmp_block_table,
+                           cu_seqlens_q, seqused_ori_kv, seqused_cmp_kv, cmp_residual_kv, ori_topk_length, nullptr,
+                           nullptr);
+  a.plan_count = (int32_t*)workspace;
+  a.plan_rows = (uint32_t*)((char*)workspace + plan_count_bytes(params->T));
+  constexpr int PLAN_THREADS = 64;
+  hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS),
+                     (size_t)a.list_pad * sizeof(uint32_t), (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int launch_gather_probe(void* stream, const void* ori_kv, const void* cmp_kv, const void* workspace,
+                                   const SparseMlaParams* params, int32_t grid, int32_t depth, int32_t balanced,
+                                   uint32_t* sums) {
+  const int status = check_sparse(params);
+  if (status) return status;
+  if (!ori_kv || !cmp_kv || !workspace || !sums) return AFA_E_NULL;
+  if (params->D != 512 || params->BM != params->H) return AFA_E_SHAPE;  // 1 KiB rows, one item per token
+  if (grid < 1 || (int64_t)grid * PROBE_ITEMS < params->T + (balanced ? grid : 0)) return AFA_E_SHAPE;
+  const int list_pad = (params->WINDOW + params->TOPK + 255) / 256 * 256;
+  const int32_t* counts = (const int32_t*)workspace;
+  const uint32_t* lists = (const uint32_t*)((const char*)workspace + plan_count_bytes(params->T));
+  const size_t lds = (size_t)PROBE_ITEMS * list_pad * sizeof(uint32_t);
+  hipStream_t s = (hipStream_t)stream;
+  const char* o = (const char*)ori_kv;
+  const char* c = (const char*)cmp_kv;
+#define AFA_PROBE(D)                                                                                          \
+  case D:                                                                                                     \
+    if (fits_lds<gather_probe_kernel<D>>(lds) != AFA_OK) return AFA_E_SHAPE;                                 \
+    hipLaunchKernelGGL(gather_probe_kernel<D>, dim3((unsigned)grid), dim3(256), lds, s, o, c, counts, lists,    \
+                       list_pad, params->T, balanced, sums);                                                  \
+    break;
+  switch (depth) {
+    AFA_PROBE(1) AFA_PROBE(2) AFA_PROBE(4) AFA_PROBE(6) AFA_PROBE(8)
+    default: return AFA_E_SHAPE;
+  }
+#undef AFA_PROBE
   return (int)hipGetLastError();
 }
 

@@ -166,6 +166,38 @@ def attention_extras(steps, warmup, flush, device, which=ATTENTION_KEYS, prewarm
     return out
 
 
+def gather_probe_extras(steps, warmup, flush, device, depths=(1, 2, 4, 8)):
+    """The gather probe on the decode configuration (B64 x 6 at 128K): the
+    planned rows of all 384 tokens streamed through LDS with no compute, at
+    several chunks (16 rows) in flight per workgroup, one workgroup per token
+    (as the one-item kernel) or 256 workgroups with equal shares. Rates: the
+    listed rows (640 per token, 1 KiB each: the reference's logical KV read
+    rate) and the unique KV rows touched (the HBM roofline basis) per second."""
+    import torch
+
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+    from ascendflow_amd.sparse_attention.probe import gather_probe, sparse_mla_plan
+
+    policy = measurement_policy(batch=64, query_tokens=6, context=131072)
+    inputs = make_inputs(policy, 131072, device=device)
+    workspace = sparse_mla_plan(inputs.tensors, policy)
+    torch.cuda.synchronize()
+    listed = int(workspace[: 4 * policy["T"]].view(torch.int32).sum().item()) * 1024
+    unique = (len(inputs.touched["ori_kv"]) + len(inputs.touched["cmp_kv"])) * 1024
+    sums = torch.empty((384, 16), dtype=torch.int32, device=device)
+    out = {"listed_bytes": listed, "unique_kv_bytes": unique}
+    for depth in depths:
+        for grid, balanced in ((384, False), (256, True)):
+            ms, _, _ = time_launches(lambda: gather_probe(inputs.tensors, policy, workspace, grid, depth, balanced, sums),
+                                     steps, warmup, flush)
+            key = f"depth{depth}_{'balanced256' if balanced else 'items384'}"
+            out[key] = {"us": round(ms * 1e3, 2), "listed_GB_s": round(listed / (ms * 1e-3) / 1e9, 1),
+                        "unique_GB_s": round(unique / (ms * 1e-3) / 1e9, 1)}
+            log(f"[bench] gather probe {key}: {ms * 1e3:.1f} us, listed {out[key]['listed_GB_s']} GB/s, "
+                f"unique {out[key]['unique_GB_s']} GB/s")
+    return out
+
+
 def cpu_threads():
     """Threads for the CPU baseline: every CPU in this process's affinity mask,
     capped by the cgroup CPU quota when one is set (more threads than the quota
@@ -265,7 +297,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", "decode768", *ATTENTION_KEYS], default=None,
+    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", "decode768", "gather", *ATTENTION_KEYS],
+                        default=None,
                         help="time one configuration only (profiling runs; the attention keys print a log only)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-attention", action="store_true", help="skip the flash/teaching attention extras")
@@ -305,6 +338,11 @@ def main():
         log(f"[bench] copy calibration: 3 neg passes of {args.copy_calibration} MiB")
         del src, dst
 
+    if args.only == "gather":
+        extras = gather_probe_extras(args.steps, args.warmup, flush, device)
+        print(json.dumps({"gather_probe": extras}), flush=True)
+        return 0
+
     if args.only in ATTENTION_KEYS:
         extras = attention_extras(args.steps, args.warmup, flush, device, which=(args.only,), prewarm=args.prewarm)
         log(f"[bench] {args.only}: {json.dumps(extras[args.only])}")
@@ -335,8 +373,10 @@ def main():
         torch.cuda.empty_cache()
 
     extras = {}
+    if not args.only:
+        extras["gather_probe"] = gather_probe_extras(args.steps, args.warmup, flush, device)
     if not args.only and not args.no_attention:
-        extras = attention_extras(args.steps, args.warmup, flush, device)
+        extras.update(attention_extras(args.steps, args.warmup, flush, device))
         if not args.no_cpu_baseline:
             cpu["fa_c2"] = cpu_flash_c2()
             log(f"[bench] CPU fa_c2: {cpu['fa_c2']['ms_full_scaled']} ms (scaled)")

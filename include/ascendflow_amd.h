@@ -184,6 +184,31 @@ int workspace_size_attention_target(uint64_t* bytes, int64_t Sq, int64_t Sk,
                                     const FaParams* params);
 int workspace_size_simple_attention(uint64_t* bytes, int64_t S, int64_t H);
 
+/* The row-list plan alone: writes the plan that launch_sparse_mla's plan
+ * kernel writes into its workspace (layout above) for every token, nothing
+ * else. The counterpart of the vendor operator's metadata-preparation stage
+ * (docs/operators/sparse-mla.md:10-14 in the reference); used to read the
+ * selection back and to drive launch_gather_probe. `workspace` needs
+ * round_up(4 T, 256) + 4 T round_up(WINDOW + TOPK, 256) bytes. */
+int launch_sparse_mla_plan(void* stream, const int32_t* cmp_sparse_indices, const int32_t* ori_block_table,
+                           const int32_t* cmp_block_table, const int32_t* cu_seqlens_q,
+                           const int32_t* seqused_ori_kv, const int32_t* seqused_cmp_kv,
+                           const int32_t* cmp_residual_kv, const int32_t* ori_topk_length, void* workspace,
+                           const SparseMlaParams* params);
+
+/* Gather probe (measurement only; the counterpart of the reference's gather
+ * micro-benchmark, benchmarks/attention/gather_dma.py): streams the 1 KiB rows
+ * listed in a plan (D = 512, one item per token: BM = H) from ori_kv/cmp_kv
+ * through LDS as the attention kernels do, with `depth` (1, 2, 4, 6 or 8)
+ * 16-row chunks in flight per workgroup and no compute, on `grid`
+ * workgroups: items interleaved (balanced = 0) or an equal share of the flat
+ * chunk stream each (balanced = 1, every item taken as long as item 0). Each
+ * workgroup takes at most 4 items. sums [grid][16]: per thread, the sum of the
+ * first dword of every row it checked (all rows streamed, mod 2^32). */
+int launch_gather_probe(void* stream, const void* ori_kv, const void* cmp_kv, const void* workspace,
+                        const SparseMlaParams* params, int32_t grid, int32_t depth, int32_t balanced,
+                        uint32_t* sums);
+
 /* Measurement helpers (no reference kernel; the reference sweeps a >= 4x L2
  * buffer before each timed launch, benchmarks/cache.py:13-92 and
  * benchmarks/cache_sweep.py:15-32). Streams `bytes` of `buffer` through the

@@ -416,3 +416,26 @@ def test_framework_op_matches_entry_and_oracle(device, variant):
     assert empty.numel() == 0 and torch.equal(out2, out)
     with pytest.raises(ValueError):
         torch.ops.ascendflow_amd.sparse_flash_mla(*args, policy["SCALE"], policy["RATIO"], ori_mask_mode=1)
+
+
+def test_plan_entry_and_gather_probe_on_decode(device):
+    """launch_sparse_mla_plan writes the oracle's selection for all 384 decode
+    tokens (B64 x 6 at 128K), and the gather probe streams exactly the planned
+    rows at every depth, interleaved and balanced (its checksum of the first
+    dword of every streamed row equals torch's)."""
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+    from ascendflow_amd.sparse_attention.probe import expected_probe_sum, gather_probe, sparse_mla_plan
+
+    print("\n[sparse] plan entry + gather probe, decode B64x6 ctx 131072", flush=True)
+    policy = measurement_policy(batch=64, query_tokens=6, context=131072)
+    inputs = make_inputs(policy, 131072, device=device)
+    workspace = sparse_mla_plan(inputs.tensors, policy)
+    torch.cuda.synchronize()
+    assert_plan_matches(workspace, metadata_view(inputs), policy, list(range(policy["T"])))
+    want = expected_probe_sum(inputs.tensors, policy, workspace)
+    for depth in (1, 2, 4, 6, 8):
+        for grid, balanced in ((384, False), (256, False), (256, True)):
+            sums = gather_probe(inputs.tensors, policy, workspace, grid, depth, balanced)
+            torch.cuda.synchronize()
+            got = int(sums.long().sum().item()) & 0xFFFFFFFF
+            assert got == want, f"probe depth {depth} grid {grid} balanced {balanced}: checksum {got:#x} != {want:#x}"
