@@ -1014,7 +1014,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
         if (cur.j > 0) {
 #pragma unroll
           for (int k = 0; k < QK_STEPS; ++k) qf[k] = qf_next[k];
-          sink = sink_next;
+          sink = sink_next * LOG2E;
         }
         m_run = sink;
         l_run = g == 0 ? 1.0f : 0.0f;  // e^(sink - m) counted once per head
@@ -1023,7 +1023,10 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
           const scalar* q_row = (const scalar*)a.q + ((size_t)item_token(cur.j + 1) * a.H + head) * D + 8 * g;
 #pragma unroll
           for (int k = 0; k < QK_STEPS; ++k) qf_next[k] = *(const x8*)(q_row + 32 * k);
-          sink_next = a.sinks[head] * LOG2E;
+          // Used (scaled) only when the next item starts: vector loads retire
+          // in order, so consuming it here would wait for all of Q's loads,
+          // a full HBM round trip at every item start.
+          sink_next = a.sinks[head];
         }
       }
       // S^T of this chunk: fragment reads LOOK_QK k-steps ahead of the MFMAs.
