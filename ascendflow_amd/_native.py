@@ -29,6 +29,7 @@ EXPORTS = (
     "launch_sparse_mla_gather",
     "launch_sparse_mla_plan",
     "launch_gather_probe",
+    "launch_sparse_topk_indices",
     "launch_attention_target",
     "launch_simple_attention",
     "kernel_config_sparse_mla",
@@ -91,6 +92,7 @@ _SIGNATURES = {
         [_P] * 4 + [ct.POINTER(SparseMlaParams), ct.c_int32, ct.c_int32, ct.c_int32, _P],
         ct.c_int,
     ),
+    "launch_sparse_topk_indices": ([_P] * 7, ct.c_int),
     "launch_attention_target": (
         [_P] * 6 + [ct.c_int64, ct.c_int64, ct.POINTER(FaParams)],
         ct.c_int,

@@ -2,6 +2,7 @@
 
 from .attention import sparse_mla
 from .gather import sparse_mla_gather
+from .indexer import sparse_topk_indices
 from .ops import sparse_flash_mla
 
-__all__ = ["sparse_mla", "sparse_mla_gather", "sparse_flash_mla"]
+__all__ = ["sparse_mla", "sparse_mla_gather", "sparse_flash_mla", "sparse_topk_indices"]

@@ -209,6 +209,29 @@ int launch_gather_probe(void* stream, const void* ori_kv, const void* cmp_kv, co
                         const SparseMlaParams* params, int32_t grid, int32_t depth, int32_t balanced,
                         uint32_t* sums);
 
+/* Top-k index selection: the producer of cmp_sparse_indices, which the
+ * reference takes as an input and leaves to the caller's indexer
+ * (docs/operators/sparse-mla.md:8,266 in the reference). scores [T][C] f32: one
+ * index score per (token, compressed position). For token t of request b
+ * (cu_seqlens_q), with n queries in b, offset j and cutoff = max(0,
+ * seqused_cmp_kv[b] RATIO + cmp_residual_kv[b] - n + j + 1) / RATIO (the
+ * causal bound of the sparse contract, docs/operators/sparse-mla.md:41-51),
+ * writes into cmp_sparse_indices [T][1][TOPK] the min(TOPK, seqused_cmp_kv[b],
+ * cutoff, C) positions p < min(cutoff, C) of largest score, ascending, then
+ * -1 (the input contract of docs/operators/sparse-mla.md:79). Ties go to the
+ * lower position; -0 equals +0; NaN ranks above +inf. */
+typedef struct SparseTopkParams {
+  int32_t B;      /* requests */
+  int32_t T;      /* query tokens */
+  int32_t TOPK;   /* selected positions per token (row length of the output) */
+  int32_t RATIO;  /* compression ratio, 1 or 2 */
+  int64_t C;      /* score columns per token (row stride of scores), < 2^31 */
+} SparseTopkParams;
+
+int launch_sparse_topk_indices(void* stream, const float* scores, const int32_t* cu_seqlens_q,
+                               const int32_t* seqused_cmp_kv, const int32_t* cmp_residual_kv,
+                               int32_t* cmp_sparse_indices, const SparseTopkParams* params);
+
 /* Measurement helpers (no reference kernel; the reference sweeps a >= 4x L2
  * buffer before each timed launch, benchmarks/cache.py:13-92 and
  * benchmarks/cache_sweep.py:15-32). Streams `bytes` of `buffer` through the

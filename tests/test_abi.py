@@ -148,6 +148,25 @@ def test_launchers_reject_null_arguments(lib):
     assert lib.launch_cache_flush(None, None, 1024) == -1
 
 
+@pytest.mark.parametrize(
+    "fields,status",
+    [
+        (dict(B=2, T=8, TOPK=512, RATIO=2, C=4096), -1),  # NULL tensors
+        (dict(B=0, T=8, TOPK=512, RATIO=2, C=4096), -2),
+        (dict(B=2, T=8, TOPK=0, RATIO=2, C=4096), -2),
+        (dict(B=2, T=8, TOPK=512, RATIO=3, C=4096), -2),
+        (dict(B=2, T=8, TOPK=512, RATIO=2, C=0), -2),
+        (dict(B=2, T=8, TOPK=512, RATIO=2, C=2**31), -2),
+    ],
+)
+def test_topk_launcher_rejects_bad_arguments_before_any_launch(lib, fields, status):
+    from ascendflow_amd.sparse_attention.indexer import SparseTopkParams
+
+    params = SparseTopkParams(**fields)
+    assert lib.launch_sparse_topk_indices(None, None, None, None, None, None, ct.byref(params)) == status
+    assert lib.launch_sparse_topk_indices(None, None, None, None, None, None, None) == -1
+
+
 def test_python_entries_check_the_reference_asserts_before_launching():
     from ascendflow_amd.sparse_attention.attention import check_policy
 

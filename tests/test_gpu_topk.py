@@ -1,0 +1,156 @@
+"""GPU parity of the top-k index selection (launch_sparse_topk_indices).
+
+Bit-exact against the oracle (oracle/topk_reference.py) on ragged requests
+with heavy ties and special values, and at the full measured shapes: the
+reference's own index distribution (benchmarks/attention/sparse_performance.py:44-47)
+recovered from indicator scores for every token, and random scores checked on
+sampled tokens against the oracle plus, for every token, the size-independent
+properties of the output (ascending, inside the cutoff, the contract's count,
+-1 after).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from ascendflow_amd.sparse_attention import sparse_topk_indices
+from ascendflow_amd.sparse_attention.inputs import make_metadata, measurement_policy
+from oracle import topk_reference as tr
+
+pytestmark = pytest.mark.gpu
+
+SPECIAL = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 3.0e38, -3.0e38, 1e-45], np.float32)
+
+
+def run(device, scores, cu, seq_cmp, residual, topk, ratio, misalign=False):
+    """One launch; also checks the 64 guard words after the output. With
+    ``misalign`` the score rows start 4 bytes past a 16-byte boundary (the
+    kernels' scalar-load path)."""
+    to = lambda a, dt: torch.as_tensor(np.ascontiguousarray(a), dtype=dt, device=device)
+    t = scores.shape[0]
+    buffer = torch.full((t * topk + 64,), 7, dtype=torch.int32, device=device)
+    out = buffer[: t * topk].view(t, 1, topk)
+    flat = torch.empty(scores.size + 4, dtype=torch.float32, device=device)
+    start = 1 if misalign else 0
+    dev_scores = flat[start : start + scores.size].view(scores.shape)
+    dev_scores.copy_(to(scores, torch.float32))
+    assert (dev_scores.data_ptr() % 16 != 0) == misalign
+    sparse_topk_indices(dev_scores, to(cu, torch.int32), to(seq_cmp, torch.int32),
+                        to(residual, torch.int32), TOPK=topk, RATIO=ratio, out=out)
+    torch.cuda.synchronize()
+    assert torch.all(buffer[t * topk :] == 7), "write past the output"
+    return out.cpu().numpy()
+
+
+def ragged(rng, b, ratio, max_cmp, max_q=6):
+    counts = rng.integers(0, max_q, b).astype(np.int32)
+    counts[0] = 0  # an empty request
+    counts[-1] = max(1, counts[-1])
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    seq_cmp = rng.integers(0, max_cmp + 1, b).astype(np.int32)
+    seq_cmp[1 % b] = max_cmp
+    residual = (rng.integers(0, ratio, b) if ratio > 1 else np.zeros(b)).astype(np.int32)
+    return cu, seq_cmp, residual
+
+
+@pytest.mark.parametrize("ratio", [1, 2])
+@pytest.mark.parametrize("shape", ["short-rows", "odd-rows", "full-rows", "misaligned", "topk-beyond"])
+def test_ragged_tied_and_special_scores_match_the_oracle(device, ratio, shape):
+    rng = np.random.default_rng(100 * ratio + len(shape))
+    max_cmp = 700
+    topk = 1000 if shape == "topk-beyond" else 96
+    cu, seq_cmp, residual = ragged(rng, 9, ratio, max_cmp)
+    t = int(cu[-1])
+    c = {"short-rows": 300, "odd-rows": 301}.get(shape, max_cmp)
+    scores = rng.integers(-3, 4, (t, c)).astype(np.float32)
+    mask = rng.random((t, c)) < 0.1
+    scores[mask] = rng.choice(SPECIAL, int(mask.sum()))
+    got = run(device, scores, cu, seq_cmp, residual, topk, ratio, misalign=shape == "misaligned")
+    expect = tr.topk_indices(scores, cu, seq_cmp, residual, topk, ratio)
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("c", [4096, 5000, 16387, 20000, 65536, 70001])
+def test_ties_spanning_many_chunks_match_the_oracle(device, c):
+    """Few distinct values: the threshold key is shared by thousands of
+    positions, so the equal keys taken are spread over the whole row. The
+    widths cover each register-resident form at and past its capacity (4K,
+    16K, 64K positions) and the streaming form beyond 64K."""
+    rng = np.random.default_rng(c)
+    cu = np.array([0, 20, 40], np.int32)
+    seq_cmp = np.array([c, c // 2], np.int32)
+    residual = np.array([1, 0], np.int32)
+    scores = rng.integers(0, 3, (40, c)).astype(np.float32)
+    got = run(device, scores, cu, seq_cmp, residual, 512, 2)
+    expect = tr.topk_indices(scores, cu, seq_cmp, residual, 512, 2)
+    assert np.array_equal(got, expect)
+
+
+def measured(name):
+    shapes = {
+        "decode-b64x6-128k": dict(batch=64, query_tokens=6, context=131072),
+        "prefill-q8k-32k": dict(batch=1, query_tokens=8192, context=32768),
+    }
+    policy = measurement_policy(**shapes[name])
+    meta = make_metadata(policy, shapes[name]["context"], seed=4102026)
+    return policy, meta, shapes[name]["context"]
+
+
+def generator_bounds(meta, context, ratio):
+    """right // R per token, from the generator's own expression (sparse_performance.py:45-46)."""
+    counts = meta["counts"]
+    bounds = []
+    for n in counts:
+        bounds.extend(context - int(n) + j + 1 for j in range(int(n)))
+    return np.asarray(bounds, np.int64) // ratio
+
+
+@pytest.mark.parametrize("name", ["decode-b64x6-128k", "prefill-q8k-32k"])
+def test_indicator_scores_recover_the_measured_indices(device, name):
+    policy, meta, context = measured(name)
+    t, ratio, topk = policy["T"], policy["RATIO"], policy["TOPK"]
+    c = context // ratio
+    gen = torch.Generator(device=device).manual_seed(7)
+    scores = torch.rand((t, c), generator=gen, device=device) * 1.99 - 1.0
+    indices = torch.as_tensor(meta["cmp_sparse_indices"], device=device).view(t, topk).long()
+    valid = indices >= 0
+    rows = torch.arange(t, device=device)[:, None].expand_as(indices)
+    scores[rows[valid], indices[valid]] = 1.5 + torch.rand(int(valid.sum()), generator=gen, device=device)
+    bound = torch.as_tensor(generator_bounds(meta, context, ratio), device=device)
+    scores[torch.arange(c, device=device)[None, :] >= bound[:, None]] = 5.0
+    args = [torch.as_tensor(meta[k], device=device) for k in ("cu_seqlens_q", "seqused_cmp_kv", "cmp_residual_kv")]
+    got = sparse_topk_indices(scores, *args, TOPK=topk, RATIO=ratio)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), torch.as_tensor(meta["cmp_sparse_indices"]))
+
+
+@pytest.mark.parametrize("name", ["decode-b64x6-128k", "prefill-q8k-32k"])
+def test_random_scores_at_full_size(device, name):
+    policy, meta, context = measured(name)
+    t, ratio, topk = policy["T"], policy["RATIO"], policy["TOPK"]
+    c = context // ratio
+    gen = torch.Generator(device=device).manual_seed(11)
+    # b16-rounded normals: ties occur, as with scores stored in b16.
+    scores = torch.randn((t, c), generator=gen, device=device).to(torch.bfloat16).float()
+    args = [torch.as_tensor(meta[k], device=device) for k in ("cu_seqlens_q", "seqused_cmp_kv", "cmp_residual_kv")]
+    got = sparse_topk_indices(scores, *args, TOPK=topk, RATIO=ratio)
+    torch.cuda.synchronize()
+    # Every token: ascending inside the cutoff, the contract's count, then -1.
+    cutoff, bound = tr.token_bounds(meta["cu_seqlens_q"], meta["seqused_cmp_kv"], meta["cmp_residual_kv"], ratio)
+    take = torch.as_tensor(np.minimum(np.minimum(topk, bound), np.minimum(cutoff, c)), device=device)
+    flat = got.view(t, topk).long()
+    slots = torch.arange(topk, device=device)[None, :]
+    used = slots < take[:, None]
+    assert torch.all(flat[~used] == -1)
+    assert torch.all((flat >= 0) == used)
+    assert torch.all(flat < torch.as_tensor(cutoff, device=device)[:, None])
+    steps = flat[:, 1:] - flat[:, :-1]
+    assert torch.all((steps > 0) | ~used[:, 1:])
+    # Sampled tokens, bit-exact against the oracle (first, last, and spread):
+    # each as a one-query request whose cutoff is the token's own.
+    sample = np.unique(np.r_[0, 1, 5, t - 1, np.linspace(0, t - 1, 40).astype(int)])
+    for token in sample:
+        row = scores[token : token + 1].cpu().numpy()
+        alone = np.array([cutoff[token]], np.int32)
+        expect = tr.topk_indices(row, np.array([0, 1], np.int32), alone, np.array([0], np.int32), topk, 1)
+        assert np.array_equal(got[token].cpu().numpy(), expect[0]), f"token {token}"
