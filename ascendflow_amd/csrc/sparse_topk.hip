@@ -11,24 +11,36 @@
 // every token, the min(TOPK, C_b, cutoff) positions of largest score among
 // [0, cutoff), ties to the lower position, in ascending order.
 //
-// One workgroup per token. The take-th largest score is found by radix
-// selection on a monotonic 32-bit key of the score: three digit passes (11,
-// 11 and 10 bits from the top), each an LDS histogram over the candidates
-// whose key starts with the digits found so far. Then every key above that
-// threshold, and the first `need` keys equal to it, are written in position
-// order using prefix sums of their counts, so the output is ascending without
-// a sort.
-//
-// Rows of up to 64K positions stay in registers (sparse_topk_resident): the
-// row is read once from HBM with 16-byte loads and every pass runs on the
-// registers, so the kernel streams the scores at HBM rate. Longer rows use
-// sparse_topk_stream, which re-reads the row for each pass.
+// One workgroup per token; the selection works on a monotonic 32-bit key of
+// each score. sparse_topk_filter (rows up to 256K positions):
+//   1. sample: one key per thread, evenly spaced over the row; a radix
+//      selection on the sample gives an estimate of the threshold, taken at
+//      1.5x the expected rank plus 8, so that a little more than `take` keys
+//      usually reach it;
+//   2. filter: one streaming pass over the row (16-byte loads, several in
+//      flight per thread) appends every key >= estimate, with its position,
+//      to an LDS buffer (wave ballots, one LDS atomic per wave and step);
+//   3. exact selection: radix selection (digits of 11, 11 and 10 bits, LDS
+//      histograms) over the buffer, giving the threshold key and how many keys
+//      equal to it are taken; if fewer than `take` keys reached the estimate,
+//      or the buffer overflowed, the same selection runs over the whole row
+//      instead, re-reading it per digit (same result, slower);
+//   4. output: keys above the threshold, and keys equal to it, set bits in two
+//      LDS bitmaps over the row's positions; one scan of the bitmaps writes
+//      the positions in ascending order, taking the first `need` equal keys.
+// The row is read once from HBM on the common path. sparse_topk_stream
+// serves longer rows: every digit, and the output, re-read the row.
 #include "common.h"
 #include "../../include/ascendflow_amd.h"
 
 namespace afa {
 
 constexpr int TK_BINS = 2048;  // widest digit: 11 bits
+constexpr int TK_UNROLL = 4;    // 4-position groups in flight per thread in a streaming pass
+constexpr int64_t TK_FILTER_MAX_C = 262144;  // two LDS bitmaps of C bits each
+// Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format,
+// no swizzle): with stride 0, a load at byte offset >= num_records returns 0.
+constexpr int BUFFER_WORD3 = 0x00020000;
 constexpr int TK_STREAM_THREADS = 256;
 
 // Order-preserving map of a float to an unsigned key: larger float, larger
@@ -42,32 +54,6 @@ __device__ __forceinline__ uint32_t score_key(float v) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Exclusive prefix sum over a workgroup of THREADS threads (wave64); the
-// total is returned in *total. scratch: THREADS / 64 ints of LDS. Starts with
-// a barrier, so scratch may be reused by consecutive calls.
-template <int THREADS>
-__device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int up = __shfl_up(incl, d);
-    if (lane >= d) incl += up;
-  }
-  __syncthreads();
-  if (lane == 63) scratch[wave] = incl;
-  __syncthreads();
-  int before = 0, sum = 0;
-#pragma unroll
-  for (int w = 0; w < THREADS / 64; ++w) {
-    const int c = scratch[w];
-    before += w < wave ? c : 0;
-    sum += c;
-  }
-  *total = sum;
-  return before + incl - v;
-}
-
 struct TopkArgs {
   const float* scores;      // [T][C]
   const int32_t* cu;        // [B + 1]
@@ -76,7 +62,6 @@ struct TopkArgs {
   int32_t* indices;         // [T][1][TOPK]
   int64_t C;                // score columns per token
   int32_t B, T, TOPK, RATIO;
-  int32_t vec4;             // rows are 16-byte aligned (C % 4 == 0, aligned base)
 };
 
 // Candidates [0, cand) of a token and how many of them it takes, after the
@@ -119,217 +104,310 @@ __device__ __forceinline__ bool trivial_selection(const TopkArgs& a, TokenBounds
   return false;
 }
 
-// One digit of the radix selection, after hist[0, bins) holds the counts of
-// the remaining keys: finds the bin holding the need-th largest remaining key
-// and returns it, with *above = the count in the bins above it. Ends with a
-// barrier, so hist may be cleared next.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int up = __shfl_up(v, d);
+    if (lane >= d) v += up;
+  }
+  return v;
+}
+
+// Exclusive prefix sums of two values over the workgroup, sharing barriers;
+// totals in total[0..1]. scratch: 2 THREADS / 64 ints of LDS.
 template <int THREADS>
-__device__ __forceinline__ int choose_bin(const int* hist, int bins, int need, int* scan_scratch, int* choice,
-                                          int* above) {
-  const int per = bins / THREADS, tid = threadIdx.x;  // thread t sums bins from the top
-  int local = 0;
-  for (int q = 0; q < per; ++q) local += hist[bins - 1 - (tid * per + q)];
-  int total = 0;
-  const int before = block_exclusive_scan<THREADS>(local, scan_scratch, &total);
-  if (before < need && before + local >= need) {
-    int acc = before;
-    for (int q = 0; q < per; ++q) {
-      const int bin = bins - 1 - (tid * per + q);
-      const int c = hist[bin];
-      if (acc + c >= need) {
-        choice[0] = bin;
-        choice[1] = acc;
-        break;
-      }
-      acc += c;
-    }
+__device__ __forceinline__ void block_exclusive_scan2(int& a, int& b, int* scratch, int* total) {
+  constexpr int WAVES = THREADS / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ia = wave_inclusive_scan(a), ib = wave_inclusive_scan(b);
+  __syncthreads();
+  if (lane == 63) {
+    scratch[wave] = ia;
+    scratch[WAVES + wave] = ib;
   }
   __syncthreads();
-  const int bin = choice[0];
-  *above = choice[1];
-  __syncthreads();
-  return bin;
+  int before_a = 0, before_b = 0, sum_a = 0, sum_b = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) {
+    const int ca = scratch[w], cb = scratch[WAVES + w];
+    before_a += w < wave ? ca : 0;
+    before_b += w < wave ? cb : 0;
+    sum_a += ca;
+    sum_b += cb;
+  }
+  total[0] = sum_a;
+  total[1] = sum_b;
+  a = before_a + ia - a;
+  b = before_b + ib - b;
 }
 
 constexpr int DIGIT_SHIFT[3] = {21, 10, 0};
 constexpr int DIGIT_WIDTH[3] = {11, 11, 10};
 
-// Resident form: THREADS threads, each holding V4 groups of 4 consecutive
-// positions (group v of thread t covers [(v THREADS + t) 4, +4)), so a row of
-// up to THREADS V4 4 positions is read once, with coalesced 16-byte loads.
-template <int THREADS, int V4>
-__global__ __launch_bounds__(THREADS) void sparse_topk_resident(TopkArgs a) {
-  constexpr int WAVES = THREADS / 64, N = V4 * 4;
-  static_assert(V4 * WAVES <= THREADS, "the chunk table is scanned by one pass of the workgroup");
-  __shared__ int hist[TK_BINS];
-  __shared__ int scan_scratch[WAVES];
-  __shared__ int choice[2];
-  __shared__ int table_gt[V4 * WAVES], table_eq[V4 * WAVES];
-  const int token = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const TokenBounds tb = token_bounds(a, token);
-  int32_t* out = a.indices + (size_t)token * a.TOPK;
-  if (trivial_selection<THREADS>(a, tb, out)) return;
-  const float* row = a.scores + (size_t)token * a.C;
+// LDS of the radix selections: two histograms, used alternately, so the one
+// for the next digit is cleared while a digit is chosen from the other.
+struct RadixLds {
+  int hist[2][TK_BINS];
+  int choice[2];  // bin of the digit, keys in the bins above it
+};
 
-  uint32_t key[N];
-#pragma unroll
-  for (int v = 0; v < V4; ++v) {
-    const int i0 = (v * THREADS + tid) * 4;
-    if (a.vec4) {
-      // i0 < cand <= C with C % 4 == 0: the whole group lies inside the row.
-      float4 f = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (i0 < tb.cand) f = *reinterpret_cast<const float4*>(row + i0);
-      key[4 * v + 0] = i0 + 0 < tb.cand ? score_key(f.x) : 0u;
-      key[4 * v + 1] = i0 + 1 < tb.cand ? score_key(f.y) : 0u;
-      key[4 * v + 2] = i0 + 2 < tb.cand ? score_key(f.z) : 0u;
-      key[4 * v + 3] = i0 + 3 < tb.cand ? score_key(f.w) : 0u;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) key[4 * v + e] = i0 + e < tb.cand ? score_key(row[i0 + e]) : 0u;
-    }
-  }
-
+// Radix selection of the rank-th largest key among those a key source
+// yields: for_each_key(f) calls f(key) for every key of the source held by
+// this thread. Returns that key, with *need_out = how many keys equal to it
+// are among the rank largest. Per digit: LDS histogram atomics, one barrier,
+// wave 0 finds the digit's bin (a scan over lanes from the top bin) while the
+// other waves clear the other histogram, one barrier. Expects
+// hist[parity] cleared and leaves hist[parity] (flipped) cleared.
+template <int THREADS, typename ForEachKey>
+__device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int rank, RadixLds& lds, int& parity,
+                                                 int* need_out) {
+  static_assert(THREADS > 64, "the histogram is cleared by the waves other than wave 0");
+  const int tid = threadIdx.x, lane = tid & 63;
   uint32_t prefix = 0, prefix_mask = 0;
-  int need = tb.take;
+  int need = rank;
 #pragma unroll
   for (int pass = 0; pass < 3; ++pass) {
     const int shift = DIGIT_SHIFT[pass], bins = 1 << DIGIT_WIDTH[pass];
-    for (int i = tid; i < bins; i += THREADS) hist[i] = 0;
+    int* hist = lds.hist[parity];
+    for_each_key([&](uint32_t k) {
+      if ((k & prefix_mask) == prefix) atomicAdd(&hist[(k >> shift) & (uint32_t)(bins - 1)], 1);
+    });
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const uint32_t k = key[j];
-      if (k != 0u && (k & prefix_mask) == prefix) atomicAdd(&hist[(k >> shift) & (uint32_t)(bins - 1)], 1);
+    if (tid < 64) {
+      // Lane l sums bins [bins - (l + 1) per, bins - l per), starting at a
+      // lane-dependent rotation so that the lanes read distinct LDS banks;
+      // the lane whose bins hold the need-th key is found by a scan over the
+      // lanes, then its bins are read one per lane and scanned the same way.
+      const int per = bins / 64;
+      int local = 0;
+      for (int q = 0; q < per; ++q) local += hist[bins - 1 - (lane * per + ((q + lane) & (per - 1)))];
+      const int incl = wave_inclusive_scan(local);
+      const int owner = (int)__builtin_ctzll(__ballot(incl - local < need && incl >= need));
+      const int above = __shfl(incl - local, owner);
+      const int count = lane < per ? hist[bins - 1 - (owner * per + lane)] : 0;
+      const int incl2 = wave_inclusive_scan(count);
+      const int q = (int)__builtin_ctzll(__ballot(lane < per && above + incl2 >= need));
+      if (lane == q) {
+        lds.choice[0] = bins - 1 - (owner * per + q);
+        lds.choice[1] = above + incl2 - count;
+      }
+    } else {
+      int* spare = lds.hist[parity ^ 1];
+      for (int i = tid - 64; i < TK_BINS; i += THREADS - 64) spare[i] = 0;
     }
     __syncthreads();
-    int above = 0;
-    const int digit = choose_bin<THREADS>(hist, bins, need, scan_scratch, choice, &above);
-    need -= above;
-    prefix |= (uint32_t)digit << shift;
+    need -= lds.choice[1];
+    prefix |= (uint32_t)lds.choice[0] << shift;
     prefix_mask |= (uint32_t)(bins - 1) << shift;
+    parity ^= 1;
   }
+  *need_out = need;
+  return prefix;
+}
 
-  // Output slot of a selected key = keys above the threshold before it in
-  // position order + min(equal keys before it, need). Position order is
-  // (group, wave, lane, element): counts per (group, wave) go through one
-  // table scan. A wave holds at most 256 keys of each kind, so the wave scans
-  // carry both counts in one word (equal << 16 | above).
-  const uint32_t threshold = prefix;
-  int packed_incl[V4];
+// One streaming pass over the candidates [0, cand) of a row read through a
+// buffer resource of range cand * 4 bytes (loads past it return zeros without
+// touching memory): f(key, position) is called by every thread of the wave
+// together, TK_UNROLL * 4 times per step, with key 0 for a position past the
+// candidates (no score maps to key 0). VEC: 16-byte loads of 4 consecutive
+// positions (rows 16-byte aligned); otherwise 4-byte loads.
+template <int THREADS, bool VEC>
+__device__ __forceinline__ int stream_position(int base, int j) {
+  const int tid = threadIdx.x;
+  return VEC ? base + ((j >> 2) * THREADS + tid) * 4 + (j & 3) : base + j * THREADS + tid;
+}
+
+template <int THREADS, bool VEC, typename F>
+__device__ __forceinline__ void stream_row(__amdgpu_buffer_rsrc_t rsrc, int cand, F f) {
+  constexpr int STEP = THREADS * 4 * TK_UNROLL;
+  for (int base = 0; base < cand; base += STEP) {
+    uint32_t w[TK_UNROLL * 4];
 #pragma unroll
-  for (int v = 0; v < V4; ++v) {
-    int packed = 0;
+    for (int u = 0; u < TK_UNROLL; ++u) {
+      if constexpr (VEC) {
+        const u32x4 x = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, stream_position<THREADS, VEC>(base, 4 * u) * 4, 0, 0));
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t k = key[4 * v + e];
-      packed += k > threshold ? 1 : (k == threshold ? 0x10000 : 0);
+        for (int e = 0; e < 4; ++e) w[4 * u + e] = x[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[4 * u + e] =
+              __builtin_amdgcn_raw_buffer_load_b32(rsrc, stream_position<THREADS, VEC>(base, 4 * u + e) * 4, 0, 0);
+      }
     }
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int up = __shfl_up(packed, d);
-      if (lane >= d) packed += up;
-    }
-    packed_incl[v] = packed;
-    if (lane == 63) {
-      table_gt[v * WAVES + wave] = packed & 0xffff;
-      table_eq[v * WAVES + wave] = packed >> 16;
+    for (int j = 0; j < TK_UNROLL * 4; ++j) {
+      const int p = stream_position<THREADS, VEC>(base, j);
+      f(p < cand ? score_key(__uint_as_float(w[j])) : 0u, p);
     }
   }
+}
+
+__device__ __forceinline__ int lane_rank(uint64_t mask) {  // set bits of mask below this lane
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// LDS buffer entries for the keys that reach the estimate.
+template <int THREADS>
+constexpr int filter_cap() {
+  return THREADS <= 256 ? 2048 : 4096;
+}
+
+template <int THREADS, bool VEC>
+__global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
+  constexpr int CAP = filter_cap<THREADS>();
+  extern __shared__ uint32_t bitmaps[];  // [2][words]: keys above the threshold, keys equal to it
+  __shared__ RadixLds radix;
+  __shared__ uint32_t buf_key[CAP];
+  __shared__ int buf_pos[CAP];
+  __shared__ int scan_scratch[2 * THREADS / 64];
+  __shared__ int reached;
+  const int token = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const TokenBounds tb = token_bounds(a, token);
+  int32_t* out = a.indices + (size_t)token * a.TOPK;
+  if (trivial_selection<THREADS>(a, tb, out)) return;
+  const int cand = tb.cand, take = tb.take, words = (cand + 31) >> 5;
+  uint32_t* above_bits = bitmaps;
+  uint32_t* equal_bits = bitmaps + words;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.scores + (size_t)token * a.C), (short)0, cand * 4, BUFFER_WORD3);
+
+  // 1. Sample: thread t reads position floor(t cand / S).
+  const int samples = min(THREADS, cand);
+  uint32_t sample = 0u;
+  if (tid < samples) {
+    const int p = (int)(((int64_t)tid * cand) / samples);
+    sample = score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, p * 4, 0, 0)));
+  }
+  for (int i = tid; i < 2 * words; i += THREADS) bitmaps[i] = 0u;
+  for (int i = tid; i < TK_BINS; i += THREADS) radix.hist[0][i] = 0;
+  if (tid == 0) reached = 0;
   __syncthreads();
-  {
-    constexpr int ENTRIES = V4 * WAVES;
-    const int g = tid < ENTRIES ? table_gt[tid] : 0, q = tid < ENTRIES ? table_eq[tid] : 0;
-    int total = 0;
-    const int g_before = block_exclusive_scan<THREADS>(g, scan_scratch, &total);
-    const int q_before = block_exclusive_scan<THREADS>(q, scan_scratch, &total);
-    if (tid < ENTRIES) {  // every read of the table happened before the scans' barriers
-      table_gt[tid] = g_before;
-      table_eq[tid] = q_before;
+  int parity = 0, unused = 0;
+  const int rank = min(samples, (int)((3 * (int64_t)take * samples) / (2 * (int64_t)cand)) + 8);
+  const uint32_t estimate = radix_select<THREADS>(
+      [&](auto f) {
+        if (tid < samples) f(sample);
+      },
+      rank, radix, parity, &unused);
+
+  // 2. Filter: keys >= estimate (>= 1, so never a position past the row).
+  stream_row<THREADS, VEC>(rsrc, cand, [&](uint32_t k, int p) {
+    const bool hit = k >= estimate;
+    const uint64_t m = __ballot(hit);
+    if (m == 0) return;  // uniform
+    int first = 0;
+    if (lane == 0) first = atomicAdd(&reached, __popcll(m));
+    first = __builtin_amdgcn_readfirstlane(first);
+    const int slot = first + lane_rank(m);
+    if (hit && slot < CAP) {
+      buf_key[slot] = k;
+      buf_pos[slot] = p;
     }
+  });
+  __syncthreads();
+  const int n = reached;
+
+  // 3. Exact selection, from the buffer when it holds every key that can be
+  // taken, else from the row; then the selected keys are marked.
+  int need = 0;
+  uint32_t threshold = 0;
+  if (n >= take && n <= CAP) {
+    threshold = radix_select<THREADS>(
+        [&](auto f) {
+          for (int i = tid; i < n; i += THREADS) f(buf_key[i]);
+        },
+        take, radix, parity, &need);
+    for (int i = tid; i < n; i += THREADS) {
+      const uint32_t k = buf_key[i];
+      const int p = buf_pos[i];
+      if (k > threshold) atomicOr(&above_bits[p >> 5], 1u << (p & 31));
+      else if (k == threshold) atomicOr(&equal_bits[p >> 5], 1u << (p & 31));
+    }
+  } else {
+    threshold = radix_select<THREADS>(
+        [&](auto f) {
+          stream_row<THREADS, VEC>(rsrc, cand, [&](uint32_t k, int) {
+            if (k != 0u) f(k);
+          });
+        },
+        take, radix, parity, &need);
+    stream_row<THREADS, VEC>(rsrc, cand, [&](uint32_t k, int p) {
+      if (k > threshold) atomicOr(&above_bits[p >> 5], 1u << (p & 31));
+      else if (k == threshold) atomicOr(&equal_bits[p >> 5], 1u << (p & 31));
+    });
   }
   __syncthreads();
-#pragma unroll
-  for (int v = 0; v < V4; ++v) {
-    int own = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t k = key[4 * v + e];
-      own += k > threshold ? 1 : (k == threshold ? 0x10000 : 0);
-    }
-    if (own == 0) continue;
-    int gt_before = table_gt[v * WAVES + wave] + (packed_incl[v] & 0xffff) - (own & 0xffff);
-    int eq_before = table_eq[v * WAVES + wave] + (packed_incl[v] >> 16) - (own >> 16);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t k = key[4 * v + e];
-      const int position = (v * THREADS + tid) * 4 + e;
-      if (k > threshold) {
-        const int at = gt_before + min(eq_before, need);
-        if (at < tb.take) out[at] = position;
-        ++gt_before;
-      } else if (k == threshold) {
-        if (eq_before < need && gt_before + eq_before < tb.take) out[gt_before + eq_before] = position;
-        ++eq_before;
+
+  // 4. Output in position order: thread t owns words [t per, (t + 1) per).
+  // Slot of a selected position = keys above the threshold before it +
+  // min(equal keys before it, need).
+  const int per = (words + THREADS - 1) / THREADS, w0 = min(words, tid * per), w1 = min(words, w0 + per);
+  int above_before = 0, equal_before = 0;
+  for (int w = w0; w < w1; ++w) {
+    above_before += __popc(above_bits[w]);
+    equal_before += __popc(equal_bits[w]);
+  }
+  int totals[2];
+  block_exclusive_scan2<THREADS>(above_before, equal_before, scan_scratch, totals);
+  for (int w = w0; w < w1; ++w) {
+    const uint32_t g = above_bits[w], q = equal_bits[w];
+    uint32_t bits = g | q;
+    while (bits) {
+      const int b = __builtin_ctz(bits);
+      bits &= bits - 1;
+      const int p = w * 32 + b;
+      if ((g >> b) & 1u) {
+        const int at = above_before + min(equal_before, need);
+        if (at < take) out[at] = p;
+        ++above_before;
+      } else {
+        if (equal_before < need && above_before + equal_before < take) out[above_before + equal_before] = p;
+        ++equal_before;
       }
     }
   }
 }
 
-// Streaming form, for rows of any length: every pass re-reads the row.
+// Streaming form, for rows of any length: every digit re-reads the row, and
+// the output is written chunk by chunk in position order (one scan per chunk
+// of THREADS positions, counting keys equal to the threshold in the high
+// half-word and keys above it in the low one).
 __global__ __launch_bounds__(TK_STREAM_THREADS) void sparse_topk_stream(TopkArgs a) {
   constexpr int THREADS = TK_STREAM_THREADS;
-  __shared__ int hist[TK_BINS];
-  __shared__ int scan_scratch[THREADS / 64];
-  __shared__ int choice[2];
+  __shared__ RadixLds radix;
+  __shared__ int scan_scratch[2 * THREADS / 64];
   const int token = blockIdx.x, tid = threadIdx.x;
   const TokenBounds tb = token_bounds(a, token);
   int32_t* out = a.indices + (size_t)token * a.TOPK;
   if (trivial_selection<THREADS>(a, tb, out)) return;
   const float* row = a.scores + (size_t)token * a.C;
   const int cand = tb.cand;
+  for (int i = tid; i < TK_BINS; i += THREADS) radix.hist[0][i] = 0;
+  __syncthreads();
+  int parity = 0, need = 0;
+  const uint32_t threshold = radix_select<THREADS>(
+      [&](auto f) {
+        for (int i = tid; i < cand; i += THREADS) f(score_key(row[i]));
+      },
+      tb.take, radix, parity, &need);
 
-  uint32_t prefix = 0, prefix_mask = 0;
-  int need = tb.take;
-#pragma unroll
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = DIGIT_SHIFT[pass], bins = 1 << DIGIT_WIDTH[pass];
-    for (int i = tid; i < bins; i += THREADS) hist[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < cand; i += THREADS) {
-      const uint32_t k = score_key(row[i]);
-      if ((k & prefix_mask) == prefix) atomicAdd(&hist[(k >> shift) & (uint32_t)(bins - 1)], 1);
-    }
-    __syncthreads();
-    int above = 0;
-    const int digit = choose_bin<THREADS>(hist, bins, need, scan_scratch, choice, &above);
-    need -= above;
-    prefix |= (uint32_t)digit << shift;
-    prefix_mask |= (uint32_t)(bins - 1) << shift;
-  }
-
-  // Chunks of THREADS positions in order; one scan per chunk counts both
-  // kinds (equal keys in the high half-word, larger keys in the low one).
-  const uint32_t threshold = prefix;
   int written = 0, equal_seen = 0;
   for (int base = 0; base < cand; base += THREADS) {
     const int i = base + tid;
     const uint32_t k = i < cand ? score_key(row[i]) : 0u;
     const bool gt = k > threshold, eq = k == threshold;  // k == 0 past the row
-    int both = 0;
-    const int before = block_exclusive_scan<THREADS>((eq ? 0x10000 : 0) | (gt ? 1 : 0), scan_scratch, &both);
+    int above = gt ? 1 : 0, equal = eq ? 1 : 0, both[2];
+    block_exclusive_scan2<THREADS>(above, equal, scan_scratch, both);
     const int eq_left = max(0, need - equal_seen);  // equal keys still to take
-    const int eq_before = before >> 16;
-    const int at = written + (before & 0xffff) + min(eq_before, eq_left);
-    if ((gt || (eq && eq_before < eq_left)) && at < tb.take) out[at] = i;
-    written += (both & 0xffff) + min(both >> 16, eq_left);
-    equal_seen += both >> 16;
+    const int at = written + above + min(equal, eq_left);
+    if ((gt || (eq && equal < eq_left)) && at < tb.take) out[at] = i;
+    written += both[0] + min(both[1], eq_left);
+    equal_seen += both[1];
     if (written >= tb.take) break;  // uniform: every thread sees the same totals
   }
-}
-
-template <int THREADS, int V4>
-static void launch_resident(const TopkArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((sparse_topk_resident<THREADS, V4>), dim3((unsigned)a.T), dim3(THREADS), 0, stream, a);
 }
 
 }  // namespace afa
@@ -355,17 +433,26 @@ extern "C" int launch_sparse_topk_indices(void* stream, const float* scores, con
   a.T = params->T;
   a.TOPK = params->TOPK;
   a.RATIO = params->RATIO;
-  a.vec4 = (params->C % 4 == 0) && (reinterpret_cast<uintptr_t>(scores) % 16 == 0);
+  const bool vec = (params->C % 4 == 0) && (reinterpret_cast<uintptr_t>(scores) % 16 == 0);
   hipStream_t s = (hipStream_t)stream;
-  // Resident capacity THREADS * V4 * 4 positions; the smallest form that holds
-  // a full row (no token has more than C candidates).
-  if (a.C <= 4096)
-    launch_resident<256, 4>(a, s);
-  else if (a.C <= 16384)
-    launch_resident<512, 8>(a, s);
-  else if (a.C <= 65536)
-    launch_resident<1024, 16>(a, s);
-  else
-    hipLaunchKernelGGL(sparse_topk_stream, dim3((unsigned)a.T), dim3(TK_STREAM_THREADS), 0, s, a);
+  const dim3 grid((unsigned)a.T);
+  if (a.C <= TK_FILTER_MAX_C) {
+    const size_t bitmap_bytes = 2 * 4 * (size_t)((a.C + 31) / 32);
+    // Rows up to 32K positions: 256 threads, more workgroups per CU; longer
+    // rows: 512 threads, more loads in flight per row.
+    if (a.C <= 32768) {
+      if (vec)
+        hipLaunchKernelGGL((sparse_topk_filter<256, true>), grid, dim3(256), bitmap_bytes, s, a);
+      else
+        hipLaunchKernelGGL((sparse_topk_filter<256, false>), grid, dim3(256), bitmap_bytes, s, a);
+    } else {
+      if (vec)
+        hipLaunchKernelGGL((sparse_topk_filter<512, true>), grid, dim3(512), bitmap_bytes, s, a);
+      else
+        hipLaunchKernelGGL((sparse_topk_filter<512, false>), grid, dim3(512), bitmap_bytes, s, a);
+    }
+  } else {
+    hipLaunchKernelGGL(sparse_topk_stream, grid, dim3(TK_STREAM_THREADS), 0, s, a);
+  }
   return (int)hipGetLastError();
 }

@@ -70,12 +70,13 @@ def test_ragged_tied_and_special_scores_match_the_oracle(device, ratio, shape):
     assert np.array_equal(got, expect)
 
 
-@pytest.mark.parametrize("c", [4096, 5000, 16387, 20000, 65536, 70001])
+@pytest.mark.parametrize("c", [4096, 5001, 16387, 65536, 262144, 300001])
 def test_ties_spanning_many_chunks_match_the_oracle(device, c):
     """Few distinct values: the threshold key is shared by thousands of
-    positions, so the equal keys taken are spread over the whole row. The
-    widths cover each register-resident form at and past its capacity (4K,
-    16K, 64K positions) and the streaming form beyond 64K."""
+    positions, so the equal keys taken are spread over the whole row (and
+    more than the filter kernel's buffer reach the estimate). The widths run
+    up to the filter kernel's 256K-position limit and past it, where the
+    streaming form takes over."""
     rng = np.random.default_rng(c)
     cu = np.array([0, 20, 40], np.int32)
     seq_cmp = np.array([c, c // 2], np.int32)
@@ -154,3 +155,26 @@ def test_random_scores_at_full_size(device, name):
         alone = np.array([cutoff[token]], np.int32)
         expect = tr.topk_indices(row, np.array([0, 1], np.int32), alone, np.array([0], np.int32), topk, 1)
         assert np.array_equal(got[token].cpu().numpy(), expect[0]), f"token {token}"
+
+
+@pytest.mark.parametrize("c", [1000, 16384, 65536])
+@pytest.mark.parametrize("case", ["estimate-holds", "estimate-too-high", "buffer-overflow"])
+def test_estimate_fallbacks(device, c, case):
+    """The filter kernel (256 threads up to 32K positions, 512 beyond)
+    estimates the threshold from one key per thread (thread t samples position
+    floor(t c / threads)) and selects from the keys that reach the estimate,
+    or from the whole row when fewer than TOPK reach it or more than its LDS
+    buffer (2048 / 4096 entries) holds. Large scores exactly on the sampled
+    positions make the estimate too high once TOPK exceeds the sample; a TOPK
+    of 5000 overflows the buffer. Every outcome must select the same."""
+    threads = 256 if c <= 32768 else 512
+    topk = {"estimate-holds": threads - 12, "estimate-too-high": threads + 88, "buffer-overflow": 5000}[case]
+    t = np.arange(threads)
+    sampled = (t * c) // threads
+    scores = np.random.default_rng(c + topk).normal(size=(2, c)).astype(np.float32)
+    scores[0, sampled] = 10.0
+    cu = np.array([0, 2], np.int32)
+    seq_cmp, residual = np.array([c], np.int32), np.array([0], np.int32)
+    got = run(device, scores, cu, seq_cmp, residual, topk, 1)
+    expect = tr.topk_indices(scores, cu, seq_cmp, residual, topk, 1)
+    assert np.array_equal(got, expect)
