@@ -198,6 +198,87 @@ def gather_probe_extras(steps, warmup, flush, device, depths=(1, 2, 4, 8)):
     return out
 
 
+TOPK_SHAPES = {
+    # Index scores over the compressed positions of the sparse configurations:
+    # one f32 score per (query token, compressed position), C = context / 2.
+    "decode": ("top-k selection B64x6 ctx131072 (C 65536)", 64, 6, 131072),
+    "prefill8k": ("top-k selection B1 Q8192 ctx32768 (C 16384)", 1, 8192, 32768),
+}
+
+
+def topk_problem(batch, queries, context, device, seed=4102026):
+    """Seeded N(0,1) index scores and the sparse metadata of one shape, with
+    the per-token candidate counts (the causal cutoff, as the sparse contract)."""
+    import numpy as np
+    import torch
+
+    t, c = batch * queries, context // 2
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    scores = torch.randn((t, c), generator=gen, device=device)
+    counts = np.full(batch, queries, np.int64)
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    offsets = np.concatenate([np.arange(queries)] * batch)
+    cand = np.minimum(c, (context - queries + offsets + 1) // 2)
+    meta = {
+        "cu_seqlens_q": torch.as_tensor(cu, device=device),
+        "seqused_cmp_kv": torch.full((batch,), context // 2, dtype=torch.int32, device=device),
+        "cmp_residual_kv": torch.full((batch,), context % 2, dtype=torch.int32, device=device),
+    }
+    return scores, meta, cand
+
+
+def topk_extras(steps, warmup, flush, device, keys=("decode", "prefill8k")):
+    """Top-k index selection (TOPK 512) on the decode and 8K-prefill shapes.
+    Algorithmic bytes: every candidate score read once (4 B) and the index rows
+    written (4 B x TOPK per token)."""
+    import torch
+
+    from ascendflow_amd.sparse_attention import sparse_topk_indices
+
+    out = {}
+    for key in keys:
+        name, b, q, ctx = TOPK_SHAPES[key]
+        scores, meta, cand = topk_problem(b, q, ctx, device)
+        indices = torch.empty((b * q, 1, 512), dtype=torch.int32, device=device)
+        launch = lambda: sparse_topk_indices(scores, meta["cu_seqlens_q"], meta["seqused_cmp_kv"],
+                                             meta["cmp_residual_kv"], TOPK=512, RATIO=2, out=indices)
+        ms, _, _ = time_launches(launch, steps, warmup, flush)
+        nbytes = int(4 * cand.sum() + 4 * b * q * 512)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[key] = {"workload": name, "us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                    "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"[bench] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        del scores, indices
+    return out
+
+
+def cpu_topk(key, sample_tokens=48):
+    """The oracle's brute-force selection (one stable lexsort per token, NumPy,
+    one thread) on a token sample of one top-k shape, scaled to all tokens."""
+    import numpy as np
+    import torch
+
+    from oracle.topk_reference import topk_indices
+
+    name, b, q, ctx = TOPK_SHAPES[key]
+    scores, meta, cand = topk_problem(b, q, ctx, torch.device("cpu"))
+    t = b * q
+    tokens = np.linspace(0, t - 1, min(sample_tokens, t)).astype(int)
+    host = scores.numpy()
+    # Each sampled token as a one-query request with its own cutoff.
+    run = lambda: [topk_indices(host[k : k + 1], np.array([0, 1], np.int32), np.array([cand[k]], np.int32),
+                                np.array([0], np.int32), 512, 1) for k in tokens]
+    seconds = median_seconds(run, 3)
+    fraction = len(tokens) / t
+    return {
+        "us_full_scaled": round(seconds / fraction * 1e6, 1),
+        "gbs": round(4 * float(cand[tokens].sum()) / seconds / 1e9, 3),
+        "sample": f"{len(tokens)} of {t} tokens of {name}, NumPy, 1 thread, median of 3 runs {seconds:.3f} s, "
+                  f"scaled by {t}/{len(tokens)}",
+    }
+
+
 def cpu_threads():
     """Threads for the CPU baseline: every CPU in this process's affinity mask,
     capped by the cgroup CPU quota when one is set (more threads than the quota
@@ -297,7 +378,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", "decode768", "gather", *ATTENTION_KEYS],
+    parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", "decode768", "gather", "topk",
+                                           *ATTENTION_KEYS],
                         default=None,
                         help="time one configuration only (profiling runs; the attention keys print a log only)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -343,6 +425,11 @@ def main():
         print(json.dumps({"gather_probe": extras}), flush=True)
         return 0
 
+    if args.only == "topk":
+        extras = topk_extras(args.steps, args.warmup, flush, device)
+        print(json.dumps({"topk": extras}), flush=True)
+        return 0
+
     if args.only in ATTENTION_KEYS:
         extras = attention_extras(args.steps, args.warmup, flush, device, which=(args.only,), prewarm=args.prewarm)
         log(f"[bench] {args.only}: {json.dumps(extras[args.only])}")
@@ -375,6 +462,11 @@ def main():
     extras = {}
     if not args.only:
         extras["gather_probe"] = gather_probe_extras(args.steps, args.warmup, flush, device)
+        extras["topk"] = topk_extras(args.steps, args.warmup, flush, device)
+        if not args.no_cpu_baseline:
+            for key in TOPK_SHAPES:
+                cpu[f"topk_{key}"] = cpu_topk(key)
+                log(f"[bench] CPU topk_{key}: {cpu[f'topk_{key}']['us_full_scaled']} us (scaled)")
     if not args.only and not args.no_attention:
         extras.update(attention_extras(args.steps, args.warmup, flush, device))
         if not args.no_cpu_baseline:

@@ -13,8 +13,10 @@ Modules:
 - ``sparse_reference``  TND/PA_BBND row selection, gather layout and FP32 sparse
                         MLA with per-head sinks, restates
                         ``benchmarks/attention/sparse_reference.py:15-181``.
-- ``sparse_inputs``     seeded long-context measurement inputs, restates
-                        ``benchmarks/attention/sparse_performance.py:27-82``.
+- ``topk_reference``    top-k index selection over index scores under the
+                        ``cmp_sparse_indices`` contract of
+                        ``docs/operators/sparse-mla.md:41-51,79`` (the reference
+                        has no indexer of its own).
 - ``attention``         FA online-softmax oracle and the teaching-attention
                         reference, restates ``benchmarks/validation/attention.py:19-121``
                         and ``benchmarks/attention/run_simple.py:115-118``.
