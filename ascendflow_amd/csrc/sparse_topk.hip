@@ -13,18 +13,20 @@
 //
 // One workgroup per token; the selection works on a monotonic 32-bit key of
 // each score. sparse_topk_filter (rows up to 256K positions):
-//   1. sample: one key per thread, evenly spaced over the row; a radix
-//      selection on the sample gives an estimate of the threshold, taken at
-//      1.5x the expected rank plus 8, so that a little more than `take` keys
-//      usually reach it;
+//   1. sample: four keys per thread, in blocks of 16 consecutive positions
+//      evenly spaced over the row; a radix selection on the sample gives an
+//      estimate of the threshold, taken at twice the expected rank plus 16,
+//      so that a few times `take` keys reach it;
 //   2. filter: one streaming pass over the row (16-byte loads, several in
 //      flight per thread) appends every key >= estimate, with its position,
 //      to an LDS buffer (wave ballots, one LDS atomic per wave and step);
 //   3. exact selection: radix selection (digits of 11, 11 and 10 bits, LDS
 //      histograms) over the buffer, giving the threshold key and how many keys
 //      equal to it are taken; if fewer than `take` keys reached the estimate,
-//      or the buffer overflowed, the same selection runs over the whole row
-//      instead, re-reading it per digit (same result, slower);
+//      or the buffer overflowed, the row is filtered again at another sample
+//      rank (binary search, up to four passes), and failing that the same
+//      selection runs over the whole row, re-reading it per digit (same
+//      result, slower);
 //   4. output: keys above the threshold, and keys equal to it, set bits in two
 //      LDS bitmaps over the row's positions; one scan of the bitmaps writes
 //      the positions in ascending order, taking the first `need` equal keys.
@@ -37,6 +39,8 @@ namespace afa {
 
 constexpr int TK_BINS = 2048;  // widest digit: 11 bits
 constexpr int TK_UNROLL = 4;    // 4-position groups in flight per thread in a streaming pass
+constexpr int TK_FILTER_ROUNDS = 4;  // filter passes before the whole-row selection
+constexpr int TK_SAMPLES = 4;        // sample keys per thread for the threshold estimate
 constexpr int64_t TK_FILTER_MAX_C = 262144;  // two LDS bitmaps of C bits each
 // Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format,
 // no swizzle): with stride 0, a load at byte offset >= num_records returns 0.
@@ -171,7 +175,18 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
     const int shift = DIGIT_SHIFT[pass], bins = 1 << DIGIT_WIDTH[pass];
     int* hist = lds.hist[parity];
     for_each_key([&](uint32_t k) {
-      if ((k & prefix_mask) == prefix) atomicAdd(&hist[(k >> shift) & (uint32_t)(bins - 1)], 1);
+      // Lanes whose key falls in the same bin as the first counting lane's add
+      // together in one atomic (keys often share their leading digit); the
+      // others add their own.
+      const bool counts = (k & prefix_mask) == prefix;
+      const uint64_t active = __ballot(counts);
+      if (active == 0) return;  // uniform
+      const int bin = (int)((k >> shift) & (uint32_t)(bins - 1));
+      const int leader = (int)__builtin_ctzll(active);
+      const int lead_bin = __shfl(bin, leader);
+      const uint64_t same = __ballot(counts && bin == lead_bin);
+      if (lane == leader) atomicAdd(&hist[lead_bin], __popcll(same));
+      else if (counts && bin != lead_bin) atomicAdd(&hist[bin], 1);
     });
     __syncthreads();
     if (tid < 64) {
@@ -274,47 +289,77 @@ __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(a.scores + (size_t)token * a.C), (short)0, cand * 4, BUFFER_WORD3);
 
-  // 1. Sample: thread t reads position floor(t cand / S).
-  const int samples = min(THREADS, cand);
-  uint32_t sample = 0u;
-  if (tid < samples) {
-    const int p = (int)(((int64_t)tid * cand) / samples);
-    sample = score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, p * 4, 0, 0)));
+  // 1. Sample: S = min(TK_SAMPLES THREADS, cand) keys in blocks of 16
+  // consecutive positions (64 bytes), the S / 16 blocks evenly spaced over
+  // the row (block b from position floor(b cand / (S / 16))), so the sample
+  // touches few cache lines; a row shorter than TK_SAMPLES THREADS is
+  // sampled whole. Thread t holds samples 4t .. 4t + 3.
+  const int samples = min(TK_SAMPLES * THREADS, cand);
+  const int blocks = samples / 16;
+  uint32_t sample[TK_SAMPLES];
+#pragma unroll
+  for (int j = 0; j < TK_SAMPLES; ++j) {
+    const int i = tid * TK_SAMPLES + j;
+    const int p = samples < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * cand) / blocks) + (i & 15);
+    sample[j] = i < samples ? score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, p * 4, 0, 0))) : 0u;
   }
   for (int i = tid; i < 2 * words; i += THREADS) bitmaps[i] = 0u;
   for (int i = tid; i < TK_BINS; i += THREADS) radix.hist[0][i] = 0;
   if (tid == 0) reached = 0;
   __syncthreads();
   int parity = 0, unused = 0;
-  const int rank = min(samples, (int)((3 * (int64_t)take * samples) / (2 * (int64_t)cand)) + 8);
-  const uint32_t estimate = radix_select<THREADS>(
-      [&](auto f) {
-        if (tid < samples) f(sample);
-      },
-      rank, radix, parity, &unused);
 
-  // 2. Filter: keys >= estimate (>= 1, so never a position past the row).
-  stream_row<THREADS, VEC>(rsrc, cand, [&](uint32_t k, int p) {
-    const bool hit = k >= estimate;
-    const uint64_t m = __ballot(hit);
-    if (m == 0) return;  // uniform
-    int first = 0;
-    if (lane == 0) first = atomicAdd(&reached, __popcll(m));
-    first = __builtin_amdgcn_readfirstlane(first);
-    const int slot = first + lane_rank(m);
-    if (hit && slot < CAP) {
-      buf_key[slot] = k;
-      buf_pos[slot] = p;
+  // 2. Filter: keys >= estimate (>= 1, so never a position past the row),
+  // the estimate being the rank-th largest sample. A rank whose estimate lets
+  // fewer than `take` keys through, or more than the buffer holds, is
+  // replaced by binary search between the ranks known to be too small and
+  // too large, and the row filtered again; when no rank is left (a row of
+  // many equal keys) the selection runs over the whole row below.
+  int rank = min(samples, (int)((2 * (int64_t)take * samples) / cand) + 16);
+  int too_few = 0, too_many = samples + 1, n = 0;
+  bool buffered = false;
+  for (int round = 0; round < TK_FILTER_ROUNDS; ++round) {
+    const uint32_t estimate = radix_select<THREADS>(
+        [&](auto f) {
+#pragma unroll
+          for (int j = 0; j < TK_SAMPLES; ++j)
+            if (tid * TK_SAMPLES + j < samples) f(sample[j]);
+        },
+        rank, radix, parity, &unused);  // ends with a barrier: every read of `reached` is done
+    if (tid == 0) reached = 0;
+    __syncthreads();
+    stream_row<THREADS, VEC>(rsrc, cand, [&](uint32_t k, int p) {
+      const bool hit = k >= estimate;
+      const uint64_t m = __ballot(hit);
+      if (m == 0) return;  // uniform
+      int first = 0;
+      if (lane == 0) first = atomicAdd(&reached, __popcll(m));
+      first = __builtin_amdgcn_readfirstlane(first);
+      const int slot = first + lane_rank(m);
+      if (hit && slot < CAP) {
+        buf_key[slot] = k;
+        buf_pos[slot] = p;
+      }
+    });
+    __syncthreads();
+    n = reached;
+    if (n >= take && n <= CAP) {
+      buffered = true;
+      break;
     }
-  });
-  __syncthreads();
-  const int n = reached;
+    if (n < take)
+      too_few = rank;
+    else
+      too_many = rank;
+    rank = too_many > samples ? min(samples, 2 * rank) : (too_few + too_many) / 2;
+    if (rank <= too_few || rank >= too_many) break;  // no rank left to try
+  }
 
   // 3. Exact selection, from the buffer when it holds every key that can be
   // taken, else from the row; then the selected keys are marked.
   int need = 0;
   uint32_t threshold = 0;
-  if (n >= take && n <= CAP) {
+  if (buffered) {
     threshold = radix_select<THREADS>(
         [&](auto f) {
           for (int i = tid; i < n; i += THREADS) f(buf_key[i]);

@@ -158,21 +158,25 @@ def test_random_scores_at_full_size(device, name):
 
 
 @pytest.mark.parametrize("c", [1000, 16384, 65536])
-@pytest.mark.parametrize("case", ["estimate-holds", "estimate-too-high", "buffer-overflow"])
+@pytest.mark.parametrize("case", ["estimate-holds", "estimate-refiltered", "estimate-too-high", "buffer-overflow"])
 def test_estimate_fallbacks(device, c, case):
     """The filter kernel (256 threads up to 32K positions, 512 beyond)
-    estimates the threshold from one key per thread (thread t samples position
-    floor(t c / threads)) and selects from the keys that reach the estimate,
-    or from the whole row when fewer than TOPK reach it or more than its LDS
-    buffer (2048 / 4096 entries) holds. Large scores exactly on the sampled
-    positions make the estimate too high once TOPK exceeds the sample; a TOPK
-    of 5000 overflows the buffer. Every outcome must select the same."""
-    threads = 256 if c <= 32768 else 512
-    topk = {"estimate-holds": threads - 12, "estimate-too-high": threads + 88, "buffer-overflow": 5000}[case]
-    t = np.arange(threads)
-    sampled = (t * c) // threads
+    estimates the threshold from S = 4 x threads sampled keys (the whole row
+    when shorter: sample i in block i // 16 of 16 consecutive positions, block
+    b starting at floor(b c / (S / 16))) and selects from the keys that reach it.
+    When fewer than TOPK reach it, or more than its LDS buffer (2048 / 4096
+    entries) holds, it filters again at another sample rank (binary search,
+    up to four passes), then selects from the whole row. Large scores on a
+    32nd of the sampled positions need further passes; on all of them the
+    estimate stays too high once TOPK exceeds the sample; a TOPK of 5000
+    overflows the buffer. Every outcome must select the same."""
+    samples = min(4 * (256 if c <= 32768 else 512), c)
+    topk = {"estimate-holds": samples // 4 - 12, "estimate-refiltered": samples // 32 + 40,
+            "estimate-too-high": samples + 88, "buffer-overflow": 5000}[case]
+    i = np.arange(samples)
+    sampled = i if samples < 4 * (256 if c <= 32768 else 512) else (i // 16) * c // (samples // 16) + i % 16
     scores = np.random.default_rng(c + topk).normal(size=(2, c)).astype(np.float32)
-    scores[0, sampled] = 10.0
+    scores[0, sampled[::32] if case == "estimate-refiltered" else sampled] = 10.0
     cu = np.array([0, 2], np.int32)
     seq_cmp, residual = np.array([c], np.int32), np.array([0], np.int32)
     got = run(device, scores, cu, seq_cmp, residual, topk, 1)
