@@ -151,9 +151,25 @@ constexpr int DIGIT_WIDTH[3] = {11, 11, 10};
 
 // LDS of the radix selections: two histograms, used alternately, so the one
 // for the next digit is cleared while a digit is chosen from the other.
+// PACKED: 16-bit counts, two bins per word, for selections over fewer than
+// 2^16 keys (a count never carries into its neighbour).
+template <bool PACKED>
 struct RadixLds {
-  int hist[2][TK_BINS];
+  static constexpr int WORDS = PACKED ? TK_BINS / 2 : TK_BINS;
+  uint32_t hist[2][WORDS];
   int choice[2];  // bin of the digit, keys in the bins above it
+  __device__ __forceinline__ void add(int parity, int bin, int n) {
+    if constexpr (PACKED)
+      atomicAdd(&hist[parity][bin >> 1], (uint32_t)n << ((bin & 1) * 16));
+    else
+      atomicAdd(&hist[parity][bin], (uint32_t)n);
+  }
+  __device__ __forceinline__ int get(int parity, int bin) const {
+    if constexpr (PACKED)
+      return (int)((hist[parity][bin >> 1] >> ((bin & 1) * 16)) & 0xffffu);
+    else
+      return (int)hist[parity][bin];
+  }
 };
 
 // Radix selection of the rank-th largest key among those a key source
@@ -163,8 +179,8 @@ struct RadixLds {
 // wave 0 finds the digit's bin (a scan over lanes from the top bin) while the
 // other waves clear the other histogram, one barrier. Expects
 // hist[parity] cleared and leaves hist[parity] (flipped) cleared.
-template <int THREADS, typename ForEachKey>
-__device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int rank, RadixLds& lds, int& parity,
+template <int THREADS, bool PACKED, typename ForEachKey>
+__device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int rank, RadixLds<PACKED>& lds, int& parity,
                                                  int* need_out) {
   static_assert(THREADS > 64, "the histogram is cleared by the waves other than wave 0");
   const int tid = threadIdx.x, lane = tid & 63;
@@ -173,7 +189,7 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
 #pragma unroll
   for (int pass = 0; pass < 3; ++pass) {
     const int shift = DIGIT_SHIFT[pass], bins = 1 << DIGIT_WIDTH[pass];
-    int* hist = lds.hist[parity];
+    const int cur = parity;
     for_each_key([&](uint32_t k) {
       // Lanes whose key falls in the same bin as the first counting lane's add
       // together in one atomic (keys often share their leading digit); the
@@ -185,8 +201,8 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
       const int leader = (int)__builtin_ctzll(active);
       const int lead_bin = __shfl(bin, leader);
       const uint64_t same = __ballot(counts && bin == lead_bin);
-      if (lane == leader) atomicAdd(&hist[lead_bin], __popcll(same));
-      else if (counts && bin != lead_bin) atomicAdd(&hist[bin], 1);
+      if (lane == leader) lds.add(cur, lead_bin, __popcll(same));
+      else if (counts && bin != lead_bin) lds.add(cur, bin, 1);
     });
     __syncthreads();
     if (tid < 64) {
@@ -196,11 +212,12 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
       // lanes, then its bins are read one per lane and scanned the same way.
       const int per = bins / 64;
       int local = 0;
-      for (int q = 0; q < per; ++q) local += hist[bins - 1 - (lane * per + ((q + lane) & (per - 1)))];
+#pragma unroll 8  // a full unroll keeps 32 loads in flight and sets the kernel's register peak
+      for (int q = 0; q < per; ++q) local += lds.get(cur, bins - 1 - (lane * per + ((q + lane) & (per - 1))));
       const int incl = wave_inclusive_scan(local);
       const int owner = (int)__builtin_ctzll(__ballot(incl - local < need && incl >= need));
       const int above = __shfl(incl - local, owner);
-      const int count = lane < per ? hist[bins - 1 - (owner * per + lane)] : 0;
+      const int count = lane < per ? lds.get(cur, bins - 1 - (owner * per + lane)) : 0;
       const int incl2 = wave_inclusive_scan(count);
       const int q = (int)__builtin_ctzll(__ballot(lane < per && above + incl2 >= need));
       if (lane == q) {
@@ -208,8 +225,8 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
         lds.choice[1] = above + incl2 - count;
       }
     } else {
-      int* spare = lds.hist[parity ^ 1];
-      for (int i = tid - 64; i < TK_BINS; i += THREADS - 64) spare[i] = 0;
+      uint32_t* spare = lds.hist[parity ^ 1];
+      for (int i = tid - 64; i < RadixLds<PACKED>::WORDS; i += THREADS - 64) spare[i] = 0u;
     }
     __syncthreads();
     need -= lds.choice[1];
@@ -270,13 +287,19 @@ constexpr int filter_cap() {
   return THREADS <= 256 ? 2048 : 4096;
 }
 
+template <bool COMPACT> struct BufferPosition { typedef int type; };
+template <> struct BufferPosition<true> { typedef uint16_t type; };
+
+// COMPACT (rows up to 32K positions, 256 threads): 16-bit histogram counts
+// and buffer positions, so that more workgroups fit in a CU's LDS.
 template <int THREADS, bool VEC>
 __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
   constexpr int CAP = filter_cap<THREADS>();
+  constexpr bool COMPACT = THREADS <= 256;
   extern __shared__ uint32_t bitmaps[];  // [2][words]: keys above the threshold, keys equal to it
-  __shared__ RadixLds radix;
+  __shared__ RadixLds<COMPACT> radix;
   __shared__ uint32_t buf_key[CAP];
-  __shared__ int buf_pos[CAP];
+  __shared__ typename BufferPosition<COMPACT>::type buf_pos[CAP];
   __shared__ int scan_scratch[2 * THREADS / 64];
   __shared__ int reached;
   const int token = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -304,7 +327,7 @@ __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
     sample[j] = i < samples ? score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, p * 4, 0, 0))) : 0u;
   }
   for (int i = tid; i < 2 * words; i += THREADS) bitmaps[i] = 0u;
-  for (int i = tid; i < TK_BINS; i += THREADS) radix.hist[0][i] = 0;
+  for (int i = tid; i < RadixLds<COMPACT>::WORDS; i += THREADS) radix.hist[0][i] = 0u;
   if (tid == 0) reached = 0;
   __syncthreads();
   int parity = 0, unused = 0;
@@ -338,7 +361,7 @@ __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
       const int slot = first + lane_rank(m);
       if (hit && slot < CAP) {
         buf_key[slot] = k;
-        buf_pos[slot] = p;
+        buf_pos[slot] = (typename BufferPosition<COMPACT>::type)p;
       }
     });
     __syncthreads();
@@ -422,7 +445,7 @@ __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
 // half-word and keys above it in the low one).
 __global__ __launch_bounds__(TK_STREAM_THREADS) void sparse_topk_stream(TopkArgs a) {
   constexpr int THREADS = TK_STREAM_THREADS;
-  __shared__ RadixLds radix;
+  __shared__ RadixLds<false> radix;
   __shared__ int scan_scratch[2 * THREADS / 64];
   const int token = blockIdx.x, tid = threadIdx.x;
   const TokenBounds tb = token_bounds(a, token);
@@ -430,7 +453,7 @@ __global__ __launch_bounds__(TK_STREAM_THREADS) void sparse_topk_stream(TopkArgs
   if (trivial_selection<THREADS>(a, tb, out)) return;
   const float* row = a.scores + (size_t)token * a.C;
   const int cand = tb.cand;
-  for (int i = tid; i < TK_BINS; i += THREADS) radix.hist[0][i] = 0;
+  for (int i = tid; i < TK_BINS; i += THREADS) radix.hist[0][i] = 0u;
   __syncthreads();
   int parity = 0, need = 0;
   const uint32_t threshold = radix_select<THREADS>(
