@@ -13,6 +13,10 @@ ascending, then ``-1`` (``docs/operators/sparse-mla.md:41-51,79``;
 cutoff, ties to the lower position. How the scores are computed (the
 indexer's own attention over compressed keys) is the caller's, as it is in the
 reference.
+
+The same call is registered as the torch custom op
+``ascendflow_amd::sparse_topk_indices`` (with a shape-only fake), so a
+framework can trace the indexer -> top-k -> ``sparse_flash_mla`` chain.
 """
 
 from __future__ import annotations
@@ -79,3 +83,22 @@ def sparse_topk_indices(scores, cu_seqlens_q, seqused_cmp_kv, cmp_residual_kv, T
     )
     _native.check(status, "launch_sparse_topk_indices")
     return out
+
+
+@torch.library.custom_op("ascendflow_amd::sparse_topk_indices", mutates_args=())
+def sparse_topk_indices_op(
+    scores: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    seqused_cmp_kv: torch.Tensor,
+    cmp_residual_kv: torch.Tensor,
+    topk: int,
+    cmp_ratio: int,
+) -> torch.Tensor:
+    """Framework-facing form of ``sparse_topk_indices``: returns a new
+    ``cmp_sparse_indices`` [T, 1, topk] int32."""
+    return sparse_topk_indices(scores, cu_seqlens_q, seqused_cmp_kv, cmp_residual_kv, TOPK=topk, RATIO=cmp_ratio)
+
+
+@sparse_topk_indices_op.register_fake
+def _(scores, cu_seqlens_q, seqused_cmp_kv, cmp_residual_kv, topk, cmp_ratio):
+    return scores.new_empty((scores.shape[0], 1, topk), dtype=torch.int32)

@@ -210,6 +210,18 @@ def test_framework_op_is_registered_with_a_shape_only_fake():
     assert empty.numel() == 0
 
 
+def test_topk_op_is_registered_with_a_shape_only_fake():
+    """ascendflow_amd::sparse_topk_indices traces on meta tensors: [T, 1, topk] int32."""
+    import torch
+
+    import ascendflow_amd.sparse_attention  # noqa: F401  registers the op
+
+    meta = torch.device("meta")
+    i32 = lambda *shape: torch.empty(*shape, dtype=torch.int32, device=meta)  # noqa: E731
+    out = torch.ops.ascendflow_amd.sparse_topk_indices(torch.empty(6, 4096, device=meta), i32(3), i32(2), i32(2), 512, 2)
+    assert out.shape == (6, 1, 512) and out.dtype == torch.int32
+
+
 def test_noalloc_entry_rejects_workspaces_beyond_its_scratch(lib):
     """A call whose workspace exceeds the 32 MiB static scratch is refused with
     AFA_E_WORKSPACE before anything is launched (a 32K-token prefill needs 100 MiB)."""

@@ -123,6 +123,9 @@ def test_indicator_scores_recover_the_measured_indices(device, name):
     got = sparse_topk_indices(scores, *args, TOPK=topk, RATIO=ratio)
     torch.cuda.synchronize()
     assert torch.equal(got.cpu(), torch.as_tensor(meta["cmp_sparse_indices"]))
+    # The framework op runs the same kernel.
+    via_op = torch.ops.ascendflow_amd.sparse_topk_indices(scores, *args, topk, ratio)
+    assert torch.equal(via_op, got)
 
 
 @pytest.mark.parametrize("name", ["decode-b64x6-128k", "prefill-q8k-32k"])
