@@ -12,7 +12,8 @@
 // [0, cutoff), ties to the lower position, in ascending order.
 //
 // One workgroup per token; the selection works on a monotonic 32-bit key of
-// each score. sparse_topk_filter (rows up to 256K positions):
+// each score. sparse_topk_filter (rows up to 256K positions; 256 threads up
+// to 32K positions, 1024 beyond):
 //   1. sample: four keys per thread, in blocks of 16 consecutive positions
 //      evenly spaced over the row; a radix selection on the sample gives an
 //      estimate of the threshold, taken at twice the expected rank plus 16,
@@ -507,7 +508,7 @@ extern "C" int launch_sparse_topk_indices(void* stream, const float* scores, con
   if (a.C <= TK_FILTER_MAX_C) {
     const size_t bitmap_bytes = 2 * 4 * (size_t)((a.C + 31) / 32);
     // Rows up to 32K positions: 256 threads, more workgroups per CU; longer
-    // rows: 512 threads, more loads in flight per row.
+    // rows: 1024 threads, more loads in flight per row.
     if (a.C <= 32768) {
       if (vec)
         hipLaunchKernelGGL((sparse_topk_filter<256, true>), grid, dim3(256), bitmap_bytes, s, a);
@@ -515,9 +516,9 @@ extern "C" int launch_sparse_topk_indices(void* stream, const float* scores, con
         hipLaunchKernelGGL((sparse_topk_filter<256, false>), grid, dim3(256), bitmap_bytes, s, a);
     } else {
       if (vec)
-        hipLaunchKernelGGL((sparse_topk_filter<512, true>), grid, dim3(512), bitmap_bytes, s, a);
+        hipLaunchKernelGGL((sparse_topk_filter<1024, true>), grid, dim3(1024), bitmap_bytes, s, a);
       else
-        hipLaunchKernelGGL((sparse_topk_filter<512, false>), grid, dim3(512), bitmap_bytes, s, a);
+        hipLaunchKernelGGL((sparse_topk_filter<1024, false>), grid, dim3(1024), bitmap_bytes, s, a);
     }
   } else {
     hipLaunchKernelGGL(sparse_topk_stream, grid, dim3(TK_STREAM_THREADS), 0, s, a);
