@@ -298,13 +298,21 @@ def cpu_threads():
 
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it (model name, family/model/stepping,
+    physical cores per socket, MHz) and the logical CPUs the host has."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, value = (part.strip() for part in line.split(":", 1))
+                fields.setdefault(key, value)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ident = "/".join(fields.get(k, "?") for k in ("cpu family", "model", "stepping"))
+    cores = fields.get("cpu cores", "?")
+    mhz = fields.get("cpu MHz", "?")
+    return f"{name} (family/model/stepping {ident}, {cores} cores per socket, {mhz} MHz, {os.cpu_count()} logical CPUs on the host)"
 
 
 def median_seconds(fn, repeats):
