@@ -16,8 +16,9 @@
 // to 32K positions, 1024 beyond):
 //   1. sample: four keys per thread, in blocks of 16 consecutive positions
 //      evenly spaced over the row; a radix selection on the sample gives an
-//      estimate of the threshold, taken at twice the expected rank plus 16,
-//      so that a few times `take` keys reach it;
+//      estimate of the threshold, taken at 1.25x the expected rank plus 8
+//      (256 threads) or twice it plus 16 (1024), so that somewhat more than
+//      `take` keys reach it;
 //   2. filter: one streaming pass over the row (16-byte loads, several in
 //      flight per thread) appends every key >= estimate, with its position,
 //      to an LDS buffer (wave ballots, one LDS atomic per wave and step);
@@ -33,6 +34,8 @@
 //      the positions in ascending order, taking the first `need` equal keys.
 // The row is read once from HBM on the common path. sparse_topk_stream
 // serves longer rows: every digit, and the output, re-read the row.
+#include <algorithm>
+
 #include "common.h"
 #include "../../include/ascendflow_amd.h"
 
@@ -42,6 +45,7 @@ constexpr int TK_BINS = 2048;  // widest digit: 11 bits
 constexpr int TK_UNROLL = 4;    // 4-position groups in flight per thread in a streaming pass
 constexpr int TK_FILTER_ROUNDS = 4;  // filter passes before the whole-row selection
 constexpr int TK_SAMPLES = 4;        // sample keys per thread for the threshold estimate
+constexpr int TK_WIDE_CAP = 4096;    // filter buffer entries of the 1024-thread form
 constexpr int64_t TK_FILTER_MAX_C = 262144;  // two LDS bitmaps of C bits each
 // Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format,
 // no swizzle): with stride 0, a load at byte offset >= num_records returns 0.
@@ -67,6 +71,8 @@ struct TopkArgs {
   int32_t* indices;         // [T][1][TOPK]
   int64_t C;                // score columns per token
   int32_t B, T, TOPK, RATIO;
+  int32_t cap;              // filter buffer entries (dynamic LDS)
+  int32_t words;            // bitmap words per row in dynamic LDS: ceil(C / 32)
 };
 
 // Candidates [0, cand) of a token and how many of them it takes, after the
@@ -282,12 +288,6 @@ __device__ __forceinline__ int lane_rank(uint64_t mask) {  // set bits of mask b
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-// LDS buffer entries for the keys that reach the estimate.
-template <int THREADS>
-constexpr int filter_cap() {
-  return THREADS <= 256 ? 2048 : 4096;
-}
-
 template <bool COMPACT> struct BufferPosition { typedef int type; };
 template <> struct BufferPosition<true> { typedef uint16_t type; };
 
@@ -295,12 +295,20 @@ template <> struct BufferPosition<true> { typedef uint16_t type; };
 // and buffer positions, so that more workgroups fit in a CU's LDS.
 template <int THREADS, bool VEC>
 __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
-  constexpr int CAP = filter_cap<THREADS>();
   constexpr bool COMPACT = THREADS <= 256;
-  extern __shared__ uint32_t bitmaps[];  // [2][words]: keys above the threshold, keys equal to it
+  typedef typename BufferPosition<COMPACT>::type Position;
+  // Dynamic LDS: two bitmaps of a.words words (keys above the threshold, keys
+  // equal to it), then (COMPACT) the buffer of a.cap keys and positions; the
+  // 1024-thread form keeps a static buffer of TK_WIDE_CAP entries.
+  extern __shared__ uint32_t dynamic_lds[];
+  __shared__ uint32_t wide_key[COMPACT ? 1 : TK_WIDE_CAP];
+  __shared__ int wide_pos[COMPACT ? 1 : TK_WIDE_CAP];
+  const int CAP = COMPACT ? a.cap : TK_WIDE_CAP;
+  uint32_t* const bitmaps = dynamic_lds;
+  uint32_t* const buf_key = COMPACT ? dynamic_lds + 2 * a.words : wide_key;
+  Position* const buf_pos =
+      COMPACT ? reinterpret_cast<Position*>(dynamic_lds + 2 * a.words + a.cap) : reinterpret_cast<Position*>(wide_pos);
   __shared__ RadixLds<COMPACT> radix;
-  __shared__ uint32_t buf_key[CAP];
-  __shared__ typename BufferPosition<COMPACT>::type buf_pos[CAP];
   __shared__ int scan_scratch[2 * THREADS / 64];
   __shared__ int reached;
   const int token = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
@@ -339,7 +347,11 @@ __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
   // replaced by binary search between the ranks known to be too small and
   // too large, and the row filtered again; when no rank is left (a row of
   // many equal keys) the selection runs over the whole row below.
-  int rank = min(samples, (int)((2 * (int64_t)take * samples) / cand) + 16);
+  // Sample rank: about 1.25x (256 threads: a buffer of 2 TOPK entries) or 2x
+  // (4096 entries) the expected count of samples above the threshold, plus a
+  // margin.
+  int rank = THREADS <= 256 ? min(samples, (int)((5 * (int64_t)take * samples) / (4 * (int64_t)cand)) + 8)
+                            : min(samples, (int)((2 * (int64_t)take * samples) / cand) + 16);
   int too_few = 0, too_many = samples + 1, n = 0;
   bool buffered = false;
   for (int round = 0; round < TK_FILTER_ROUNDS; ++round) {
@@ -362,7 +374,7 @@ __global__ __launch_bounds__(THREADS) void sparse_topk_filter(TopkArgs a) {
       const int slot = first + lane_rank(m);
       if (hit && slot < CAP) {
         buf_key[slot] = k;
-        buf_pos[slot] = (typename BufferPosition<COMPACT>::type)p;
+        buf_pos[slot] = (Position)p;
       }
     });
     __syncthreads();
@@ -505,20 +517,26 @@ extern "C" int launch_sparse_topk_indices(void* stream, const float* scores, con
   const bool vec = (params->C % 4 == 0) && (reinterpret_cast<uintptr_t>(scores) % 16 == 0);
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)a.T);
+  a.words = (int32_t)((a.C + 31) / 32);
+  // Buffer: rows up to 32K positions (16-bit positions) hold 2 TOPK entries,
+  // between 1024 and 8192, so that little of a CU's LDS is spent on it at the
+  // usual TOPK; longer rows hold TK_WIDE_CAP.
+  a.cap = a.C <= 32768 ? (int32_t)std::min<int64_t>(8192, std::max<int64_t>(1024, ((int64_t)a.TOPK * 2 + 255) / 256 * 256))
+                       : TK_WIDE_CAP;
   if (a.C <= TK_FILTER_MAX_C) {
-    const size_t bitmap_bytes = 2 * 4 * (size_t)((a.C + 31) / 32);
+    const size_t dynamic_bytes = 2 * 4 * (size_t)a.words + (a.C <= 32768 ? (size_t)a.cap * 6 : 0);
     // Rows up to 32K positions: 256 threads, more workgroups per CU; longer
     // rows: 1024 threads, more loads in flight per row.
     if (a.C <= 32768) {
       if (vec)
-        hipLaunchKernelGGL((sparse_topk_filter<256, true>), grid, dim3(256), bitmap_bytes, s, a);
+        hipLaunchKernelGGL((sparse_topk_filter<256, true>), grid, dim3(256), dynamic_bytes, s, a);
       else
-        hipLaunchKernelGGL((sparse_topk_filter<256, false>), grid, dim3(256), bitmap_bytes, s, a);
+        hipLaunchKernelGGL((sparse_topk_filter<256, false>), grid, dim3(256), dynamic_bytes, s, a);
     } else {
       if (vec)
-        hipLaunchKernelGGL((sparse_topk_filter<1024, true>), grid, dim3(1024), bitmap_bytes, s, a);
+        hipLaunchKernelGGL((sparse_topk_filter<1024, true>), grid, dim3(1024), dynamic_bytes, s, a);
       else
-        hipLaunchKernelGGL((sparse_topk_filter<1024, false>), grid, dim3(1024), bitmap_bytes, s, a);
+        hipLaunchKernelGGL((sparse_topk_filter<1024, false>), grid, dim3(1024), dynamic_bytes, s, a);
     }
   } else {
     hipLaunchKernelGGL(sparse_topk_stream, grid, dim3(TK_STREAM_THREADS), 0, s, a);

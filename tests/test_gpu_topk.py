@@ -167,15 +167,15 @@ def test_estimate_fallbacks(device, c, case):
     estimates the threshold from S = 4 x threads sampled keys (the whole row
     when shorter: sample i in block i // 16 of 16 consecutive positions, block
     b starting at floor(b c / (S / 16))) and selects from the keys that reach it.
-    When fewer than TOPK reach it, or more than its LDS buffer (2048 / 4096
-    entries) holds, it filters again at another sample rank (binary search,
+    When fewer than TOPK reach it, or more than its LDS buffer holds (2 TOPK
+    entries within [1024, 8192] up to 32K positions, 4096 beyond), it filters again at another sample rank (binary search,
     up to four passes), then selects from the whole row. Large scores on a
     32nd of the sampled positions need further passes; on all of them the
-    estimate stays too high once TOPK exceeds the sample; a TOPK of 5000
+    estimate stays too high once TOPK exceeds the sample; a TOPK of 9000
     overflows the buffer. Every outcome must select the same."""
     samples = min(4 * (256 if c <= 32768 else 1024), c)
     topk = {"estimate-holds": samples // 4 - 12, "estimate-refiltered": samples // 32 + 40,
-            "estimate-too-high": samples + 88, "buffer-overflow": 5000}[case]
+            "estimate-too-high": samples + 88, "buffer-overflow": 9000}[case]
     i = np.arange(samples)
     sampled = i if samples < 4 * (256 if c <= 32768 else 1024) else (i // 16) * c // (samples // 16) + i % 16
     scores = np.random.default_rng(c + topk).normal(size=(2, c)).astype(np.float32)
@@ -184,4 +184,18 @@ def test_estimate_fallbacks(device, c, case):
     seq_cmp, residual = np.array([c], np.int32), np.array([0], np.int32)
     got = run(device, scores, cu, seq_cmp, residual, topk, 1)
     expect = tr.topk_indices(scores, cu, seq_cmp, residual, topk, 1)
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("topk", [2048, 4000])
+def test_large_topk_matches_the_oracle(device, topk):
+    """Rows up to 32K positions size the filter buffer to 2 TOPK entries (up to
+    8192), so large selections stay on the buffered path."""
+    rng = np.random.default_rng(topk)
+    c = 16384
+    cu = np.array([0, 24, 48], np.int32)
+    seq_cmp, residual = np.array([c, c // 2 + 1000], np.int32), np.array([1, 0], np.int32)
+    scores = rng.normal(size=(48, c)).astype(np.float32)
+    got = run(device, scores, cu, seq_cmp, residual, topk, 2)
+    expect = tr.topk_indices(scores, cu, seq_cmp, residual, topk, 2)
     assert np.array_equal(got, expect)
