@@ -42,6 +42,7 @@ EXPORTS = (
     "workspace_size_attention_target",
     "workspace_size_simple_attention",
     "launch_cache_flush",
+    "launch_clock_probe",
     "ascendflow_amd_version",
 )
 
@@ -114,6 +115,7 @@ _SIGNATURES = {
         ct.c_int,
     ),
     "launch_cache_flush": ([_P, _P, ct.c_uint64], ct.c_int),
+    "launch_clock_probe": ([_P, _P, ct.c_int32], ct.c_int),
     "ascendflow_amd_version": ([], ct.c_char_p),
 }
 

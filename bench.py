@@ -206,6 +206,42 @@ TOPK_SHAPES = {
 }
 
 
+def device_figures(device):
+    """The shader clock the GPU runs at under an ALU load (launch_clock_probe:
+    shader cycles over the 100 MHz real-time counter while every SIMD runs
+    FMAs; MFMA-heavy kernels run lower, as their PMC cycle counts in profiles/
+    show) and a measured stream-copy bandwidth (a 1 GiB device-to-device copy,
+    read plus write bytes over its HIP-event time, median of 5)."""
+    import torch
+
+    from ascendflow_amd import _native
+
+    lib = _native.library()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    out = torch.zeros(5, dtype=torch.int64, device=device)
+    clocks = []
+    for _ in range(3):
+        _native.check(lib.launch_clock_probe(stream, out.data_ptr(), 200000), "launch_clock_probe")
+        torch.cuda.synchronize()
+        c0, c1, r0, r1 = (int(v) for v in out[:4].tolist())
+        clocks.append(100.0 * (c1 - c0) / max(1, r1 - r0))
+    src = torch.ones((1 << 30) // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    times = []
+    for _ in range(6):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        dst.copy_(src)
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    copy_ms = statistics.median(times[1:])
+    del src, dst
+    return {"shader_clock_mhz_valu_load": round(statistics.median(clocks), 1),
+            "stream_copy_gbs": round(2 * (1 << 30) / (copy_ms * 1e-3) / 1e9, 1),
+            "stream_copy": "1 GiB float32 device-to-device copy (read + write bytes), median of 5 after one warm-up"}
+
+
 def topk_problem(batch, queries, context, device, seed=4102026):
     """Seeded N(0,1) index scores and the sparse metadata of one shape, with
     the per-token candidate counts (the causal cutoff, as the sparse contract)."""
@@ -384,7 +420,7 @@ def cpu_flash_c2(heads=2):
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--steps", type=int, default=30)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--only", choices=["prefill8k", "decode", "prefill32k", "decode768", "gather", "topk",
                                            *ATTENTION_KEYS],
@@ -469,6 +505,9 @@ def main():
 
     extras = {}
     if not args.only:
+        extras["device"] = device_figures(device)
+        log(f"[bench] device: {extras['device']['shader_clock_mhz_valu_load']} MHz shader clock under ALU load, "
+            f"{extras['device']['stream_copy_gbs']} GB/s stream copy")
         extras["gather_probe"] = gather_probe_extras(args.steps, args.warmup, flush, device)
         extras["topk"] = topk_extras(args.steps, args.warmup, flush, device)
         if not args.no_cpu_baseline:

@@ -238,6 +238,13 @@ int launch_sparse_topk_indices(void* stream, const float* scores, const int32_t*
  * caches with a read-modify-write so the next launch starts cold. */
 int launch_cache_flush(void* stream, void* buffer, uint64_t bytes);
 
+/* Measurement helper (no reference kernel): runs `spins` dependent FMAs in
+ * every thread of 1024 workgroups of 256 (every SIMD busy) and writes, from
+ * workgroup 0, out[0..1] = the shader-cycle counter before and after and
+ * out[2..3] = the 100 MHz real-time counter before and after (out has 5
+ * entries): the shader clock is 100 MHz x (out[1] - out[0]) / (out[3] - out[2]). */
+int launch_clock_probe(void* stream, uint64_t* out, int32_t spins);
+
 /* Library version string. */
 const char* ascendflow_amd_version(void);
 

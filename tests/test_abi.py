@@ -146,6 +146,8 @@ def test_launchers_reject_null_arguments(lib):
     assert lib.launch_attention_target(None, p, p, p, p, None, 8, 8, ct.byref(fa)) == -2
     assert lib.launch_simple_attention(None, p, p, p, p, None, 100, 1) == -2
     assert lib.launch_cache_flush(None, None, 1024) == -1
+    assert lib.launch_clock_probe(None, None, 1000) == -1
+    assert lib.launch_clock_probe(None, ct.c_void_p(16), 0) == -2
 
 
 @pytest.mark.parametrize(
