@@ -199,3 +199,22 @@ def test_large_topk_matches_the_oracle(device, topk):
     got = run(device, scores, cu, seq_cmp, residual, topk, 2)
     expect = tr.topk_indices(scores, cu, seq_cmp, residual, topk, 2)
     assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("c,topk", [(1, 1), (3, 2), (4, 1), (7, 16), (33, 33)])
+def test_tiny_rows_many_empty_requests(device, c, topk):
+    """Rows of 1-33 positions (the scalar and the 16-byte load paths), TOPK 1
+    and TOPK equal to the row, 40 requests of which most are empty, and a
+    request holding a single token."""
+    rng = np.random.default_rng(c * 100 + topk)
+    counts = np.zeros(40, np.int32)
+    counts[[3, 17, 18, 39]] = (2, 1, 3, 1)
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    seq_cmp = rng.integers(0, c + 1, 40).astype(np.int32)
+    residual = rng.integers(0, 2, 40).astype(np.int32)
+    t = int(cu[-1])
+    scores = rng.integers(-2, 3, (t, c)).astype(np.float32)
+    for ratio in (1, 2):
+        got = run(device, scores, cu, seq_cmp, residual if ratio == 2 else np.zeros_like(residual), topk, ratio)
+        expect = tr.topk_indices(scores, cu, seq_cmp, residual if ratio == 2 else np.zeros_like(residual), topk, ratio)
+        assert np.array_equal(got, expect), ratio
