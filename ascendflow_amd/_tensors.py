@@ -47,12 +47,16 @@ def _span(tensor):
 
 
 def check_disjoint(named):
-    """Every written tensor must not overlap any other external tensor."""
+    """Every written tensor must not overlap any other external tensor (read
+    tensors may share memory with each other, as read-only caches do)."""
     spans = [(name, *_span(t), write) for name, t, write in named if t.numel()]
     for i, (a, a0, a1, aw) in enumerate(spans):
-        for b, b0, b1, bw in spans[i + 1 :]:
-            if (aw or bw) and a0 < b1 and b0 < a1:
-                raise ValueError(f"external tensors {a} and {b} overlap")
+        if not aw:
+            continue
+        for j, (b, b0, b1, _) in enumerate(spans):
+            if j != i and a0 < b1 and b0 < a1:
+                first, second = (a, b) if i < j else (b, a)
+                raise ValueError(f"external tensors {first} and {second} overlap")
 
 
 def stream_handle(device) -> int:

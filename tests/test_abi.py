@@ -234,3 +234,20 @@ def test_noalloc_entry_rejects_workspaces_beyond_its_scratch(lib):
     assert lib.launch_sparse_mla_noalloc(*args, ct.byref(big)) == -4
     assert lib.launch_sparse_mla_noalloc(*args, ct.byref(good_params(D=64))) == -2
     assert lib.launch_sparse_mla_noalloc(*args, None) == -1
+
+
+def test_disjointness_check_covers_written_tensors_only():
+    """A written tensor may overlap nothing; read tensors may share memory
+    (src/runtime/torch.py:94-167 checks the same disjointness)."""
+    import torch
+
+    from ascendflow_amd._tensors import check_disjoint
+
+    buf = torch.zeros(64)
+    a, b, c = buf[0:16], buf[8:24], buf[32:48]
+    check_disjoint([("a", a, False), ("b", b, False), ("c", c, True)])  # reads overlap: allowed
+    with pytest.raises(ValueError, match="a and b overlap"):
+        check_disjoint([("a", a, False), ("b", b, True), ("c", c, False)])
+    with pytest.raises(ValueError, match="a and c overlap"):
+        check_disjoint([("a", buf[0:40], False), ("b", b, False), ("c", c, True)])
+    check_disjoint([("a", a, True), ("e", buf[0:0], False)])  # empty tensors never overlap
