@@ -218,3 +218,33 @@ def test_tiny_rows_many_empty_requests(device, c, topk):
         got = run(device, scores, cu, seq_cmp, residual if ratio == 2 else np.zeros_like(residual), topk, ratio)
         expect = tr.topk_indices(scores, cu, seq_cmp, residual if ratio == 2 else np.zeros_like(residual), topk, ratio)
         assert np.array_equal(got, expect), ratio
+
+
+@pytest.mark.parametrize("ratio", [1, 2])
+def test_selected_indices_drive_sparse_mla(device, ratio):
+    """The chain the top-k step serves: index scores -> sparse_topk_indices ->
+    sparse_mla. The indices the kernel selects meet the operator's input
+    contract, so the attention over them matches the oracle run on the same
+    indices (rows bit-exact through the operator's own selection image)."""
+    from ascendflow_amd.sparse_attention import sparse_mla
+    from oracle import sparse_reference as sr
+    from tests.sparse_helpers import assert_close, call_args, call_kwargs, expected_rows, to_device
+
+    policy = sr.default_policy(B=3, T=12, RATIO=ratio, MAX_SEQ=2048, ORI_BLOCKS=48, CMP_BLOCKS=48)
+    data = sr.inputs(policy, "ragged")
+    t, c = policy["T"], policy["MAX_SEQ"] // ratio
+    scores = np.random.default_rng(ratio).normal(size=(t, c)).astype(np.float32)
+    meta = {k: torch.as_tensor(data[k], device=device) for k in ("cu_seqlens_q", "seqused_cmp_kv", "cmp_residual_kv")}
+    indices = sparse_topk_indices(torch.as_tensor(scores, device=device), meta["cu_seqlens_q"], meta["seqused_cmp_kv"],
+                                  meta["cmp_residual_kv"], TOPK=policy["TOPK"], RATIO=ratio)
+    torch.cuda.synchronize()
+    data["cmp_sparse_indices"] = indices.cpu().numpy()
+    assert np.array_equal(data["cmp_sparse_indices"],
+                          tr.topk_indices(scores, data["cu_seqlens_q"], data["seqused_cmp_kv"], data["cmp_residual_kv"],
+                                          policy["TOPK"], ratio))
+    tensors = to_device(data, policy, device)
+    debug = torch.empty((t, policy["S"], 2), dtype=torch.int32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug)
+    torch.cuda.synchronize()
+    assert np.array_equal(debug.cpu().numpy(), expected_rows(data, policy, list(range(t))))
+    assert_close(tensors["attention_out"].float().cpu().numpy(), sr.oracle_fp32(data, policy), policy["DTYPE"])
