@@ -219,7 +219,9 @@ int launch_gather_probe(void* stream, const void* ori_kv, const void* cmp_kv, co
  * writes into cmp_sparse_indices [T][1][TOPK] the min(TOPK, seqused_cmp_kv[b],
  * cutoff, C) positions p < min(cutoff, C) of largest score, ascending, then
  * -1 (the input contract of docs/operators/sparse-mla.md:79). Ties go to the
- * lower position; -0 equals +0; NaN ranks above +inf. */
+ * lower position; -0 equals +0; NaN ranks above +inf. Returns AFA_E_SHAPE for
+ * B, T, TOPK or C <= 0, C >= 2^31 or RATIO not 1 or 2, AFA_E_NULL for a NULL
+ * pointer, before any launch. One launch; no workspace. */
 typedef struct SparseTopkParams {
   int32_t B;      /* requests */
   int32_t T;      /* query tokens */
