@@ -123,6 +123,15 @@ __device__ __forceinline__ uint32_t opaque_uniform(uint32_t v) {
 // s_waitcnt immediate for lgkmcnt(0) alone (gfx9 encoding: vmcnt[3:0] |
 // expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14, all other fields at max).
 constexpr int WAIT_LGKM0 = 0xC07F;
+// s_waitcnt vmcnt(N) alone: wait until at most N vector memory operations of
+// this wave are in flight. The counter retires loads, loads to LDS and stores
+// of a wave in issue order (the compiler's own waits behind a mix of loads and
+// stores assume the same), so this waits for all but the N most recent.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
 // Workgroup barrier without the memory fence of __syncthreads(): global loads
 // of later chunks stay in flight across it. The caller's own LDS stores are
 // complete (lgkmcnt(0)) before it signals; the empty asm statements keep the

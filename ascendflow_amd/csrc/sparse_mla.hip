@@ -340,35 +340,41 @@ constexpr float TAU = 8.0f;
 
 // Stores one 16-head tile of O, held as the PV accumulators hold it (lane
 // (i16, g) has features 16t + 4g + 0..3 of head i16, t < DPV / 16), scaled by
-// inv and rounded, through a wave-private LDS stage of 16 * DPV * 2 bytes, so
-// that each global store writes whole DPV * 2-byte head-row slices (full cache
-// lines). Stored straight from the accumulators, every instruction would write
-// 16 scattered 32-byte pieces; measured on prefill Q8K, that pattern costs ~9%
-// of the kernel. 16-byte units are XOR-swizzled by head row in the stage. The
+// inv and rounded, through a wave-private LDS stage, so that each global store
+// writes whole DPV * 2-byte head-row slices (full cache lines). Stored straight
+// from the accumulators, every instruction would write 16 scattered 32-byte
+// pieces; measured on prefill Q8K, that pattern costs ~9% of the kernel.
+// Head row h of the stage starts at stage + h * STAGE_ROW and holds 16-byte
+// unit u of the head row at unit (unit_base + u) ^ (h & SWZ): packed
+// (STAGE_ROW = DPV * 2, unit_base 0, SWZ = units - 1), or the wave's own
+// feature units of a KV ring tile (STAGE_ROW = the tile's row bytes, unit_base
+// = the wave's first feature unit, SWZ = 15: the tile's own swizzle). The
 // stage is only touched by this wave, whose LDS operations complete in order.
-template <int DT, int DPV>
-__device__ __forceinline__ void store_head_tile(uint32_t stage, const f32x4 (&o)[DPV / 16], float inv,
-                                                typename B16<DT>::scalar* out, size_t head_stride, int lane) {
+template <int DT, int DPV, int STAGE_ROW = DPV * 2, int SWZ = DPV / 8 - 1>
+__device__ __forceinline__ void store_head_tile(uint32_t stage, uint32_t unit_base, const f32x4 (&o)[DPV / 16],
+                                                float inv, typename B16<DT>::scalar* out, size_t head_stride,
+                                                int lane) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x4 x4;
   constexpr int PVT = DPV / 16;
-  constexpr int UR = DPV / 8;       // 16-byte units per head row
-  constexpr int ROWB = DPV * 2;     // bytes per head row
-  constexpr int HPI = 1024 / ROWB;  // head rows per 1 KiB wave access
+  constexpr int UR = DPV / 8;            // 16-byte units per head row
+  constexpr int HPI = 1024 / (DPV * 2);  // head rows per 1 KiB wave access
   static_assert((UR & (UR - 1)) == 0 && 16 % HPI == 0, "power-of-two head rows of at most 1 KiB");
+  static_assert(STAGE_ROW >= DPV * 2 && (SWZ == UR - 1 || SWZ == 15), "stage rows hold a head row each");
   const int i16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < PVT; ++t) {
     x4 v;
 #pragma unroll
     for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[t][k] * inv);
-    const uint32_t unit = (uint32_t)((2 * t + (g >> 1)) ^ (i16 & (UR - 1)));
-    *(AFA_LDS x4*)(uintptr_t)(stage + (uint32_t)(i16 * ROWB) + unit * 16u + (uint32_t)(g & 1) * 8u) = v;
+    const uint32_t unit = (unit_base + (uint32_t)(2 * t + (g >> 1))) ^ (uint32_t)(i16 & SWZ);
+    *(AFA_LDS x4*)(uintptr_t)(stage + (uint32_t)(i16 * STAGE_ROW) + unit * 16u + (uint32_t)(g & 1) * 8u) = v;
   }
 #pragma unroll
   for (int r = 0; r < 16 / HPI; ++r) {
     const int h = r * HPI + lane / UR, u = lane % UR;
-    const u32x4 w = *(const AFA_LDS u32x4*)(uintptr_t)(stage + (uint32_t)(h * ROWB) + (uint32_t)((u ^ (h & (UR - 1))) << 4));
+    const uint32_t unit = (unit_base + (uint32_t)u) ^ (uint32_t)(h & SWZ);
+    const u32x4 w = *(const AFA_LDS u32x4*)(uintptr_t)(stage + (uint32_t)(h * STAGE_ROW) + (unit << 4));
     *(u32x4*)((char*)(out + (size_t)h * head_stride) + u * 16) = w;
   }
 }
@@ -781,7 +787,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
     for (int ht = 0; ht < NQ; ++ht)
-      store_head_tile<DT, DPV>(stage, o[ht], linv_lds[16 * ht + i16], out0 + (size_t)16 * ht * D, D, lane);
+      store_head_tile<DT, DPV>(stage, 0u, o[ht], linv_lds[16 * ht + i16], out0 + (size_t)16 * ht * D, D, lane);
   }
 }
 
@@ -837,10 +843,6 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   __shared__ float alpha_lds[2][BMH];
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];
   __shared__ float ml_lds[2][2][BMH];  // item parity: running max (log2 units), denominator
-  // Output stage of the whole-item stores (store_head_tile), one 16-head tile
-  // per output wave; the 4-tile ring leaves no room for it (direct stores).
-  constexpr bool STAGED = NS == 3;
-  __shared__ __attribute__((aligned(16))) uint8_t out_stage[STAGED ? NP * 16 * DPV * 2 : 16];
   __shared__ __attribute__((aligned(16))) int count_lds[LISTS];
   extern __shared__ __attribute__((aligned(16))) uint32_t lists[];  // [LISTS][list_pad]
 
@@ -1127,27 +1129,22 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       tr_base[b] = (uint32_t)(rt * ROW_BYTES + (((dbase / 8 + 2 * b + ((i16 & 3) >> 1)) ^ (rt & 15)) << 4) + (i16 & 1) * 8);
 
     // Output of item j: this lane holds heads head0 + 16ht + i16, features
-    // dbase + 16t + 4g + i.
-    auto finish = [&](int j) {
+    // dbase + 16t + 4g + i. The stores are staged (store_head_tile) in this
+    // wave's own feature units of rows 0..15 of the ring tile whose PV just
+    // ended: during this step only output waves read that tile, each its own
+    // feature units (the tile swizzle XORs the unit with row & 15, which keeps
+    // it among the wave's units, or in row-by-row groups of as many units), and
+    // the fetch that refills the tile is issued after the next barrier.
+    static_assert(CHUNK >= 16, "a head tile's stage rows fit a ring tile");
+    auto finish = [&](int j, uint32_t tile) {
       const int key = item_key(j), par = j & 1;
       const int token = key / head_tiles, head0 = (key % head_tiles) * a.BM;
       scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
       for (int ht = 0; ht < NQ; ++ht) {
         const float inv = 1.0f / ml_lds[par][1][16 * ht + i16];
-        if constexpr (STAGED) {
-          store_head_tile<DT, DPV>(lds_address(out_stage) + (uint32_t)(ow * 16 * DPV * 2), o[ht], inv,
-                                   out0 + (size_t)16 * ht * D, D, lane);
-        } else {
-          scalar* out_row = out0 + (size_t)(16 * ht + i16) * D + 4 * g;
-#pragma unroll
-          for (int t = 0; t < PVT; ++t) {
-            x4 v;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = (scalar)(o[ht][t][k] * inv);
-            *(x4*)(out_row + 16 * t) = v;
-          }
-        }
+        store_head_tile<DT, DPV, ROW_BYTES, 15>(tile, (uint32_t)(dbase / 8), o[ht], inv, out0 + (size_t)16 * ht * D,
+                                                D, lane);
       }
     };
 
@@ -1157,12 +1154,14 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
     for (int s = 0;; ++s) {
       const bool score_active = cur.j < J;
       if (!score_active && !ovalid) break;
-      // KV(s) has landed once at most the younger fetch batch is in flight
-      // (stores and loads may complete out of order: wait for all after stores).
+      // KV(s) has landed once at most the younger fetch batch is in flight.
+      // After output stores, wait for those too: the counter retires in issue
+      // order, so waiting for KV(s) alone would do, but letting the stores run
+      // on into the next step measured ~2% slower on prefill.
       if (stored || !ahead_loaded)
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        wait_vmcnt<0>();
       else
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+        wait_vmcnt<PIECES>();
       block_barrier();
       stored = false;
       ahead_loaded = false;
@@ -1216,7 +1215,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
           __builtin_amdgcn_sched_barrier(0);
         }
         if (ocur.c == ocur.chunks() - 1) {
-          finish(ocur.j);
+          finish(ocur.j, tile);
           stored = true;
         }
       }
