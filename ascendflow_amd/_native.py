@@ -65,6 +65,7 @@ class SparseMlaParams(ct.Structure):
         ("dtype", ct.c_int32),
         ("scale", ct.c_float),
         ("parts", ct.c_int32),
+        ("ring", ct.c_int32),
         ("debug_rows", ct.c_void_p),
         ("softmax_lse", ct.c_void_p),
     ]

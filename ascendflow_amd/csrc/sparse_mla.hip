@@ -78,6 +78,7 @@ struct SparseArgs {
   int32_t list_pad;      // row-list capacity: WINDOW + TOPK rounded up to 256 (whole KiB)
   int32_t parts;         // parts each split (token, head tile) key is divided into (one-item kernel)
   int32_t split_from;    // first split (token, head tile) key; keys below it run whole
+  int32_t ring;          // KV ring tiles of the persistent kernel (3 or 4)
   float scale;
 };
 
@@ -805,7 +806,8 @@ struct Cursor {
 // pipeline drain and no dependent global round trip.
 //  - the KV ring of NS tiles, P slots and step parities run on across items;
 //    output waves fetch KV rows AHEAD = NS - 2 chunks ahead of the score waves
-//    (the host launches the 3-tile ring, one chunk in flight);
+//    (3 tiles: one chunk in flight, for rows re-read from the caches; 4: two,
+//    for rows streamed from HBM);
 //  - output waves copy the row list (and count) of item j + LISTS - 1 when
 //    item j starts, into a ring of LISTS LDS lists;
 //  - score waves load Q and the sinks of item j + 1 into registers when item j
@@ -1438,6 +1440,7 @@ static int check_sparse(const SparseMlaParams* p) {
   if ((int64_t)p->CMP_BLOCKS * (p->PAGE / p->RATIO) >= (int64_t)CMP_BIT) return AFA_E_SHAPE;
   if (!(p->scale > 0.0f)) return AFA_E_SHAPE;
   if (p->parts < 0 || p->parts > MAX_PARTS) return AFA_E_SHAPE;
+  if (p->ring != 0 && p->ring != 3 && p->ring != 4) return AFA_E_SHAPE;
   if ((int64_t)p->T * (p->H / p->BM) * MAX_PARTS > 0x7fffffffLL) return AFA_E_SHAPE;
   return AFA_OK;
 }
@@ -1494,6 +1497,18 @@ static Split choose_split(const SparseMlaParams* p) {
   return best;
 }
 
+// MI355X's Infinity Cache (the memory-side cache in front of HBM). Caches
+// larger than it stream mostly from HBM, where two chunks in flight (a 4-tile
+// ring) pay: decode B86 / B128 / B170 / B256 x 6 at 128K 9% / 2.4% / 4.3% /
+// 5.3% faster, B128 x 6 at 32K 2.8%, a 4 x 2K prefill at 128K 1.3%; caches
+// that fit it are re-read from it, where the 3-tile ring measured 3-4% faster
+// (prefill Q8K and Q2K at 32K).
+constexpr uint64_t INFINITY_CACHE_BYTES = uint64_t(256) << 20;
+static uint64_t kv_cache_bytes(const SparseMlaParams* p) {
+  const uint64_t rows = (uint64_t)p->ORI_BLOCKS * p->PAGE + (uint64_t)p->CMP_BLOCKS * (p->PAGE / p->RATIO);
+  return rows * (uint64_t)p->D * 2u;
+}
+
 static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void* ori_kv,
                             const void* cmp_kv, const int32_t* idx, const int32_t* ot,
                             const int32_t* ct, const int32_t* cu, const int32_t* so,
@@ -1535,6 +1550,7 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   const Split split = choose_split(p);
   a.parts = split.parts;
   a.split_from = (int32_t)split.split_from;
+  a.ring = p->ring != 0 ? p->ring : (kv_cache_bytes(p) > INFINITY_CACHE_BYTES ? 4 : 3);
   a.scale = p->scale;
   return a;
 }
@@ -1592,22 +1608,28 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
     // Plan kernel, then the persistent kernel over the plan when every CU gets
     // at least two items (the persistent form removes the per-item start,
     // which outweighs a second kernel only then) and its row-list ring fits
-    // next to its KV ring. The 3-tile ring leaves room for the staged output
-    // stores; with them and the role priorities it measured faster than the
-    // 4-tile ring at every stream length (decode B86, B128 and B170 x 6: 1%,
-    // 4% and 1%). Otherwise (and for split keys) the one-item-per-workgroup
-    // kernel resolves its own rows.
+    // next to its KV ring: a.ring tiles (4 keeps two chunks in flight, for
+    // rows streamed from HBM) where the row-list ring of 5 lists fits next to
+    // them, else 3 (4 lists). Otherwise (and for split keys) the
+    // one-item-per-workgroup kernel resolves its own rows.
     static const int cus = device_cus();
     const int64_t items = tiles;
-    if (items >= 2 * (int64_t)cus && fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>>(4 * lds) == AFA_OK) {
-      constexpr int PLAN_THREADS = 64;
-      hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return (int)e;
-      const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
-      hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64),
-                         4 * lds, stream, a);
-      return (int)hipGetLastError();
+    if (items >= 2 * (int64_t)cus) {
+      const bool four = a.ring == 4 && fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>>(5 * lds) == AFA_OK;
+      if (four || fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>>(4 * lds) == AFA_OK) {
+        constexpr int PLAN_THREADS = 64;
+        hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+        const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
+        if (four)
+          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>), dim3(grid), dim3((NQ + NP) * 64),
+                             5 * lds, stream, a);
+        else
+          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64),
+                             4 * lds, stream, a);
+        return (int)hipGetLastError();
+      }
     }
   }
   // One workgroup per item (whole keys, then the parts of split keys): a
@@ -1869,6 +1891,6 @@ extern "C" const char* kernel_metadata_sparse_mla(void) {
          "\"parameters\":[],"
          "\"params_struct\":{\"name\":\"SparseMlaParams\",\"fields\":[\"B\",\"T\",\"H\",\"D\","
          "\"PAGE\",\"RATIO\",\"MAX_SEQ\",\"ORI_BLOCKS\",\"CMP_BLOCKS\",\"WINDOW\",\"TOPK\",\"S\","
-         "\"BM\",\"dtype\",\"scale\",\"parts\",\"debug_rows\",\"softmax_lse\"]},"
+         "\"BM\",\"dtype\",\"scale\",\"parts\",\"ring\",\"debug_rows\",\"softmax_lse\"]},"
          "\"workspace\":true}";
 }

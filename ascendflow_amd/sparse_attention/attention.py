@@ -38,7 +38,7 @@ def check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PA
 
 
 def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows=None,
-                parts=0, softmax_lse=None):
+                parts=0, softmax_lse=None, ring=0):
     return _native.SparseMlaParams(
         B=B,
         T=T,
@@ -56,6 +56,7 @@ def make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW
         dtype=_native.AFA_DTYPE[dtype],
         scale=SCALE,
         parts=parts,
+        ring=ring,
         debug_rows=None if debug_rows is None else debug_rows.data_ptr(),
         softmax_lse=None if softmax_lse is None else softmax_lse.data_ptr(),
     )
@@ -130,6 +131,7 @@ def sparse_mla(
     parts=None,
     softmax_lse=None,
     workspace=None,
+    ring=None,
 ):
     """Sparse MLA forward; writes ``attention_out`` [T, H, D] and returns it.
 
@@ -150,6 +152,12 @@ def sparse_mla(
     into k parts whose partial results a merge kernel combines. By default only
     the tokens of an incomplete last round over the 256 CUs are split, where
     that shortens the longest per-CU stream (decode-sized batches).
+
+    ``ring`` (optional, 3 or 4) fixes the KV ring of the persistent kernel on
+    the plan path: 3 tiles of 32 rows (one chunk in flight) or 4 (two, where
+    the row lists fit next to them). By default 4 when ``ori_kv`` and
+    ``cmp_kv`` together exceed the 256 MiB Infinity Cache, else 3. The output
+    does not depend on it.
 
     ``workspace`` (optional uint8 device tensor of at least
     ``workspace_bytes(...)`` bytes) replaces the per-call allocation. When
@@ -186,8 +194,9 @@ def sparse_mla(
         check_tensor("softmax_lse", softmax_lse, (T, H), torch.float32, device)
         check_disjoint([(name, t, False) for name, t in tensors.items()] + [("softmax_lse", softmax_lse, True)])
     require(parts is None or parts in range(1, 9), "parts must be None or 1..8")
+    require(ring in (None, 3, 4), "ring must be None, 3 or 4")
     params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows,
-                         parts or 0, softmax_lse)
+                         parts or 0, softmax_lse, ring or 0)
     lib = _native.library()
     # The workspace holds the per-token row-list plan (see workspace_size_sparse_mla);
     # the caching allocator hands it out in stream order, so no host sync.

@@ -59,6 +59,14 @@ typedef struct SparseMlaParams {
    * deterministic for a given value. No counterpart in the reference, whose
    * sizes are compile-time constants. */
   int32_t parts;
+  /* KV ring of the persistent kernel (the plan path): 0 = automatic, 3 or 4
+   * tiles of 32 rows. Three tiles keep one chunk in flight, four keep two.
+   * Automatic takes four when ori_kv and cmp_kv together exceed MI355X's
+   * 256 MiB Infinity Cache (rows then mostly come from HBM), else three; four
+   * tiles are used only where the row-list ring fits next to them in LDS
+   * (otherwise three). Results are bit-identical either way. No counterpart
+   * in the reference. */
+  int32_t ring;
   /* Optional debug image of the row selection, NULL normally: int32 [T, S, 2].
    * Entry r < n of token t is the r-th row of the compacted row list the
    * attention kernel streams for t (the LDS list it attends over, copied out

@@ -121,6 +121,8 @@ def good_params(**overrides):
         ({"RATIO": 3}, -2),
         ({"S": 100}, -2),
         ({"scale": 0.0}, -2),
+        ({"ring": 2}, -2),
+        ({"ring": 5}, -2),
         ({"dtype": 7}, -3),
         ({"ORI_BLOCKS": 1 << 24}, -2),
         # No gather slot at all: nothing to stream (the row lists would be empty).

@@ -125,18 +125,21 @@ def workspace_for(policy, device, parts=None):
     return torch.full((workspace_bytes(**kw, parts=parts),), 0xCD, dtype=torch.uint8, device=device)
 
 
+@pytest.mark.parametrize("ring", [3, 4])
 @pytest.mark.parametrize("variant", list(PERSISTENT_VARIANTS))
-def test_persistent_stream_matches_fused_and_oracle(device, variant):
+def test_persistent_stream_matches_fused_and_oracle(device, variant, ring):
     """T = 544 tokens: at least two work items per CU, so the plan path runs
     the persistent kernel, whose workgroups stream many tokens (and, with
     BM = 32, both head tiles of a token) through one pipeline. With one part
     its output must equal the in-kernel row resolution bit for bit; with the
     tokens split over 2 or 4 workgroups (partial results merged, 3-tile ring)
     it must match the oracle on a sample that includes empty and one-row
-    selections (the split runs on the one-item kernel, then the merge)."""
+    selections (the split runs on the one-item kernel, then the merge).
+    ``ring``: the persistent kernel's KV ring of 3 or 4 tiles (one or two
+    chunks in flight), whichever the automatic choice would take."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
-    print(f"\n[sparse] persistent stream variant={variant}", flush=True)
+    print(f"\n[sparse] persistent stream variant={variant} ring={ring}", flush=True)
     policy = sr.default_policy(**dict(dict(B=6, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160),
                                       **PERSISTENT_VARIANTS[variant]))
     data = sr.inputs(policy, "mixed")
@@ -149,7 +152,7 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
     tensors["attention_out"].fill_(float("nan"))
     lse.fill_(float("nan"))
     workspace = workspace_for(policy, device, parts=1)
-    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse, workspace=workspace)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse, workspace=workspace, ring=ring)
     torch.cuda.synchronize()
     assert guard_intact(tensors), "kernel wrote past attention_out"
     assert torch.equal(fused, tensors["attention_out"]), "persistent stream differs from the in-kernel row resolution"
@@ -177,9 +180,10 @@ def test_persistent_stream_matches_fused_and_oracle(device, variant):
         assert_lse(lse[index], lse_ref)
 
 
+@pytest.mark.parametrize("ring", [3, 4])
 @pytest.mark.parametrize("variant", ["bf16-d512-bm64-r2", "f16-d256-bm64-r1"])
 @pytest.mark.parametrize("case", sr.CASES)
-def test_validation_cases_on_the_persistent_stream(device, case, variant):
+def test_validation_cases_on_the_persistent_stream(device, case, variant, ring):
     """The eight validation cases (sparse_reference.py:45-104) at B8 x T544,
     i.e. more than two work items per CU, so the plain call takes the plan
     kernel + persistent kernel: empty selections, a ragged batch with an empty
@@ -187,10 +191,11 @@ def test_validation_cases_on_the_persistent_stream(device, case, variant):
     through one continuous chunk stream per CU. The plan it streamed must equal
     the oracle's selection for every token, its output and softmax_lse must be
     bit-identical to the one-item kernel (whose own row list is checked through
-    the debug image) and match the oracle on a sample."""
+    the debug image) and match the oracle on a sample. ``ring``: 3 or 4 KV
+    ring tiles in the persistent kernel."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
-    print(f"\n[sparse] persistent case={case} variant={variant}", flush=True)
+    print(f"\n[sparse] persistent case={case} variant={variant} ring={ring}", flush=True)
     policy = sr.default_policy(B=8, T=544, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
     policy["SCALE"] = policy["D"] ** -0.5
     data = sr.inputs(policy, case)
@@ -205,7 +210,7 @@ def test_validation_cases_on_the_persistent_stream(device, case, variant):
     tensors["attention_out"].fill_(float("nan"))
     lse = torch.full_like(lse_one, float("nan"))
     workspace = workspace_for(policy, device, parts=1)
-    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse, workspace=workspace)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse, workspace=workspace, ring=ring)
     torch.cuda.synchronize()
     assert guard_intact(tensors), "kernel wrote past attention_out"
     for k, v in before.items():
@@ -253,7 +258,8 @@ def check_measured(inputs, tokens, device, split=False, plan=False):
     match the oracle on ``tokens``. The debug image (the one-item kernel's
     streamed row list) must equal the oracle's selection for every token; with
     ``plan`` the plain call ran the plan + persistent path, and the plan it
-    streamed (read back from the workspace) must too."""
+    streamed (read back from the workspace) must too, and forcing either KV
+    ring of the persistent kernel (3 or 4 tiles) must not change a bit."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
     policy = inputs.policy
@@ -265,6 +271,10 @@ def check_measured(inputs, tokens, device, split=False, plan=False):
     meta = metadata_view(inputs)
     if plan:
         assert_plan_matches(workspace, meta, policy, every)
+        for ring in (3, 4):
+            sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), workspace=workspace, ring=ring)
+            torch.cuda.synchronize()
+            assert torch.equal(plain, inputs.tensors["attention_out"]), f"ring {ring} changed the output"
     del workspace
     debug = torch.full((policy["T"], policy["S"], 2), -7, dtype=torch.int32, device=device)
     sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), debug_rows=debug)
