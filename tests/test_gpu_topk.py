@@ -220,6 +220,25 @@ def test_tiny_rows_many_empty_requests(device, c, topk):
         assert np.array_equal(got, expect), ratio
 
 
+@pytest.mark.parametrize("c,b", [(700, 255), (700, 300), (40000, 1023), (40000, 1100)])
+def test_requests_up_to_and_beyond_one_per_thread(device, c, b):
+    """Request lookup with B just under and over the workgroup's thread count
+    (256 threads up to 32K positions, 1024 beyond): one cu entry per thread,
+    or every thread counting a strided share and one thread reading the
+    request's values. Most requests are empty; tokens sit in the first, the
+    last and a few requests between."""
+    rng = np.random.default_rng(c + b)
+    counts = np.zeros(b, np.int32)
+    counts[[0, 1, b // 2, b // 2 + 1, b - 2, b - 1]] = (2, 0, 3, 1, 0, 2)
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    seq_cmp = rng.integers(c // 2, c + 1, b).astype(np.int32)
+    residual = rng.integers(0, 2, b).astype(np.int32)
+    t = int(cu[-1])
+    scores = rng.integers(-50, 50, (t, c)).astype(np.float32)
+    got = run(device, scores, cu, seq_cmp, residual, 64, 2)
+    assert np.array_equal(got, tr.topk_indices(scores, cu, seq_cmp, residual, 64, 2))
+
+
 @pytest.mark.parametrize("ratio", [1, 2])
 def test_selected_indices_drive_sparse_mla(device, ratio):
     """The chain the top-k step serves: index scores -> sparse_topk_indices ->
