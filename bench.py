@@ -27,6 +27,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
+# Published effective TFLOPS of the reference's DSv4.1 sparse-MLA table
+# (Ascend 910B3, README.md:33-36): the basis of vs_baseline.
+REFERENCE_TFLOPS = {"prefill8k": 100.4, "prefill32k": 99.7, "decode": 78.5, "decode768": 79.5}
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 FLUSH_BYTES = 1 << 30       # > 4x the 256 MiB Infinity Cache
 
@@ -547,7 +550,9 @@ def main():
         "ms_per_step": head["ms"],
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        # The reference's published effective TFLOPS for the same configuration
+        # (Ascend 910B3, README.md:33-36; the same FLOP convention, README.md:38).
+        "vs_baseline": (round(head["tflops"] / REFERENCE_TFLOPS[head_key], 3) if head_key in REFERENCE_TFLOPS else None),
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)*0.1 Q/KV, sorted top-k without replacement, zero caches with touched rows patched)",
         "config": {
@@ -567,6 +572,7 @@ def main():
         "cpu_baseline": baseline,
         "extra": {k: {kk: vv for kk, vv in v.items() if kk != "_inputs"} for k, v in results.items()},
         "reference_ascend_910b3_ms": {"prefill8k": 6.847, "prefill32k": 27.225, "decode": 0.410, "decode768": 0.810},
+        "reference_ascend_910b3_tflops": REFERENCE_TFLOPS,
     }
     record["extra"].update(extras)
     if cpu:
