@@ -28,6 +28,7 @@ EXPORTS = (
     "launch_sparse_mla_noalloc",
     "launch_sparse_mla_gather",
     "launch_sparse_mla_plan",
+    "launch_sparse_mla_planned",
     "launch_gather_probe",
     "launch_sparse_topk_indices",
     "launch_attention_target",
@@ -90,6 +91,7 @@ _SIGNATURES = {
     "launch_sparse_mla_noalloc": ([_P] * 14 + [ct.POINTER(SparseMlaParams)], ct.c_int),
     "launch_sparse_mla_gather": ([_P] * 13 + [ct.POINTER(SparseMlaParams)], ct.c_int),
     "launch_sparse_mla_plan": ([_P] * 10 + [ct.POINTER(SparseMlaParams)], ct.c_int),
+    "launch_sparse_mla_planned": ([_P] * 7 + [ct.POINTER(SparseMlaParams)], ct.c_int),
     "launch_gather_probe": (
         [_P] * 4 + [ct.POINTER(SparseMlaParams), ct.c_int32, ct.c_int32, ct.c_int32, _P],
         ct.c_int,

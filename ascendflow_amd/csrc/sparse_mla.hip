@@ -1600,6 +1600,33 @@ static int device_cus() {
   return cus;
 }
 
+// KV ring of the persistent kernel for these arguments: a.ring tiles (4 keeps
+// two chunks in flight, for rows streamed from HBM) where the row-list ring of
+// 5 lists fits next to them, else 3 (4 lists); 0 when neither fits.
+template <int DT, int D, int NQ, int NP>
+static int persistent_ring(const SparseArgs& a) {
+  const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
+  if (a.ring == 4 && fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>>(5 * lds) == AFA_OK) return 4;
+  return fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>>(4 * lds) == AFA_OK ? 3 : 0;
+}
+
+// The persistent kernel over the plan at a.plan_count / a.plan_rows: one
+// workgroup per CU (at most one per item).
+template <int DT, int D, int NQ, int NP>
+static int launch_persistent(const SparseArgs& a, int ring, hipStream_t stream) {
+  const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
+  static const int cus = device_cus();
+  const int64_t items = (int64_t)a.T * (a.H / a.BM);
+  const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
+  if (ring == 4)
+    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>), dim3(grid), dim3((NQ + NP) * 64), 5 * lds,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64), 4 * lds,
+                       stream, a);
+  return (int)hipGetLastError();
+}
+
 template <int DT, int D, int NQ, int NP>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
@@ -1607,29 +1634,17 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   if (a.plan_rows != nullptr && a.parts == 1) {
     // Plan kernel, then the persistent kernel over the plan when every CU gets
     // at least two items (the persistent form removes the per-item start,
-    // which outweighs a second kernel only then) and its row-list ring fits
-    // next to its KV ring: a.ring tiles (4 keeps two chunks in flight, for
-    // rows streamed from HBM) where the row-list ring of 5 lists fits next to
-    // them, else 3 (4 lists). Otherwise (and for split keys) the
+    // which outweighs a second kernel only then) and a KV ring with its
+    // row-list ring fits. Otherwise (and for split keys) the
     // one-item-per-workgroup kernel resolves its own rows.
     static const int cus = device_cus();
-    const int64_t items = tiles;
-    if (items >= 2 * (int64_t)cus) {
-      const bool four = a.ring == 4 && fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>>(5 * lds) == AFA_OK;
-      if (four || fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>>(4 * lds) == AFA_OK) {
-        constexpr int PLAN_THREADS = 64;
-        hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return (int)e;
-        const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
-        if (four)
-          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>), dim3(grid), dim3((NQ + NP) * 64),
-                             5 * lds, stream, a);
-        else
-          hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64),
-                             4 * lds, stream, a);
-        return (int)hipGetLastError();
-      }
+    const int ring = persistent_ring<DT, D, NQ, NP>(a);
+    if (tiles >= 2 * (int64_t)cus && ring != 0) {
+      constexpr int PLAN_THREADS = 64;
+      hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS), lds, stream, a);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return (int)e;
+      return launch_persistent<DT, D, NQ, NP>(a, ring, stream);
     }
   }
   // One workgroup per item (whole keys, then the parts of split keys): a
@@ -1802,6 +1817,43 @@ extern "C" int launch_sparse_mla_plan(void* stream, const int32_t* cmp_sparse_in
   hipLaunchKernelGGL((sparse_plan_kernel<PLAN_THREADS>), dim3((unsigned)a.T), dim3(PLAN_THREADS),
                      (size_t)a.list_pad * sizeof(uint32_t), (hipStream_t)stream, a);
   return (int)hipGetLastError();
+}
+
+template <int DT>
+static int dispatch_planned(const SparseArgs& a, hipStream_t s) {
+  auto run = [&](auto launch_ring, auto launch) {
+    const int ring = launch_ring(a);
+    return ring == 0 ? (int)AFA_E_SHAPE : launch(a, ring, s);
+  };
+  const bool four = a.BM == 64;
+  switch (a.D) {
+    case 128:
+      return four ? run(persistent_ring<DT, 128, 4, 4>, launch_persistent<DT, 128, 4, 4>)
+                  : run(persistent_ring<DT, 128, 2, 2>, launch_persistent<DT, 128, 2, 2>);
+    case 256:
+      return four ? run(persistent_ring<DT, 256, 4, 4>, launch_persistent<DT, 256, 4, 4>)
+                  : run(persistent_ring<DT, 256, 2, 2>, launch_persistent<DT, 256, 2, 2>);
+    default:
+      return four ? run(persistent_ring<DT, 512, 4, 4>, launch_persistent<DT, 512, 4, 4>)
+                  : run(persistent_ring<DT, 512, 2, 2>, launch_persistent<DT, 512, 2, 2>);
+  }
+}
+
+extern "C" int launch_sparse_mla_planned(void* stream, const void* q, const void* ori_kv, const void* cmp_kv,
+                                         const float* sinks, void* attention_out, const void* workspace,
+                                         const SparseMlaParams* params) {
+  const int status = check_sparse(params);
+  if (status) return status;
+  if (params->debug_rows != nullptr) return AFA_E_SHAPE;  // the plan path writes no debug image
+  if (!q || !ori_kv || !cmp_kv || !sinks || !attention_out || !workspace) return AFA_E_NULL;
+  SparseArgs a = make_args(params, q, ori_kv, cmp_kv, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                           nullptr, sinks, attention_out);
+  a.plan_count = (int32_t*)workspace;
+  a.plan_rows = (uint32_t*)((char*)workspace + plan_count_bytes(params->T));
+  a.parts = 1;
+  a.split_from = a.T * (a.H / a.BM);
+  hipStream_t s = (hipStream_t)stream;
+  return params->dtype == AFA_DTYPE_BF16 ? dispatch_planned<DT_BF16>(a, s) : dispatch_planned<DT_F16>(a, s);
 }
 
 extern "C" int launch_gather_probe(void* stream, const void* ori_kv, const void* cmp_kv, const void* workspace,

@@ -219,6 +219,48 @@ def sparse_mla(
     return attention_out
 
 
+def sparse_mla_planned(q, ori_kv, cmp_kv, sinks, attention_out, workspace, B, T, H=64, D=512, PAGE=128, RATIO=2,
+                       MAX_SEQ=4096, ORI_BLOCKS=128, CMP_BLOCKS=128, WINDOW=128, TOPK=512, S=640, BM=64, DTYPE="bf16",
+                       SCALE=0.04419417382415922, *, softmax_lse=None, ring=None):
+    """The attention over a row-list plan alone (``launch_sparse_mla_planned``).
+
+    ``workspace`` holds the plan of the same metadata, written by
+    ``launch_sparse_mla_plan`` (``probe.sparse_mla_plan``) or by a plain
+    ``sparse_mla`` call that took the plan path (``plan_layout``). Writes
+    ``attention_out`` (and ``softmax_lse``) exactly as ``sparse_mla`` does on
+    the same inputs, with the persistent kernel whatever ``T`` is, and returns
+    it. ``ring`` as in ``sparse_mla``.
+    """
+    dtype = storage_dtype(DTYPE)
+    require(BM in (32, 64) and H % BM == 0, "complete head tiles")
+    require(D in (128, 256, 512), "gfx950 kernel supports D in {128, 256, 512}")
+    require(ring in (None, 3, 4), "ring must be None, 3 or 4")
+    b16 = DTYPES[dtype]
+    device = q.device
+    check_tensor("q", q, (T, H, D), b16, device)
+    check_tensor("ori_kv", ori_kv, (ORI_BLOCKS, PAGE, 1, D), b16, device)
+    check_tensor("cmp_kv", cmp_kv, (CMP_BLOCKS, PAGE // RATIO, 1, D), b16, device)
+    check_tensor("sinks", sinks, (H,), torch.float32, device)
+    check_tensor("attention_out", attention_out, (T, H, D), b16, device)
+    _, rows_at, entries = plan_layout(T, WINDOW, TOPK)
+    require(isinstance(workspace, torch.Tensor) and workspace.dtype == torch.uint8 and workspace.is_contiguous()
+            and workspace.device == device, "workspace must be a contiguous uint8 tensor on the operands' device")
+    require(workspace.numel() >= rows_at + 4 * T * entries, "workspace is smaller than the plan")
+    named = [("q", q, False), ("ori_kv", ori_kv, False), ("cmp_kv", cmp_kv, False), ("sinks", sinks, False),
+             ("workspace", workspace, False), ("attention_out", attention_out, True)]
+    if softmax_lse is not None:
+        check_tensor("softmax_lse", softmax_lse, (T, H), torch.float32, device)
+        named.append(("softmax_lse", softmax_lse, True))
+    check_disjoint(named)
+    params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE,
+                         None, 1, softmax_lse, ring or 0)
+    status = _native.library().launch_sparse_mla_planned(
+        stream_handle(device), q.data_ptr(), ori_kv.data_ptr(), cmp_kv.data_ptr(), sinks.data_ptr(),
+        attention_out.data_ptr(), workspace.data_ptr(), ct.byref(params))
+    _native.check(status, "launch_sparse_mla_planned")
+    return attention_out
+
+
 def workspace_bytes(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, DTYPE="bf16",
                     SCALE=0.04419417382415922, parts=None):
     """Bytes of the optional workspace of one call (``workspace_size_sparse_mla``)."""

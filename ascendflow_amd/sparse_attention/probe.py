@@ -2,7 +2,8 @@
 
 ``sparse_mla_plan`` runs only the plan kernel of ``launch_sparse_mla`` and
 returns its workspace (per-token selected-row counts and tagged row lists,
-layout in ``include/ascendflow_amd.h``). ``gather_probe`` streams those rows
+layout in ``include/ascendflow_amd.h``), which
+``ascendflow_amd.sparse_attention.sparse_mla_planned`` then attends over. ``gather_probe`` streams those rows
 through LDS the way the attention kernels do, with no compute, at a chosen
 number of chunks in flight: the counterpart of the reference's standalone
 gather micro-benchmark (``benchmarks/attention/gather_dma.py``), used to
@@ -27,14 +28,18 @@ def _params(policy):
     return make_params(*(policy[k] for k in keys), storage_dtype(policy["DTYPE"]), policy["SCALE"], parts=1)
 
 
-def sparse_mla_plan(tensors, policy):
-    """The row-list plan of one call (a uint8 workspace tensor) for the metadata in ``tensors``."""
+def sparse_mla_plan(tensors, policy, workspace=None):
+    """The row-list plan of one call (a uint8 workspace tensor, allocated
+    unless given) for the metadata in ``tensors``."""
     params = _params(policy)
     t = policy["T"]
     entries = -(-(policy["WINDOW"] + policy["TOPK"]) // 256) * 256
     nbytes = -(-4 * t // 256) * 256 + 4 * t * entries
     device = tensors["cmp_sparse_indices"].device
-    workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if workspace is None:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    require(workspace.dtype == torch.uint8 and workspace.is_contiguous() and workspace.numel() >= nbytes
+            and workspace.device == device, "workspace must be a contiguous uint8 tensor holding the plan")
     names = ("cmp_sparse_indices", "ori_block_table", "cmp_block_table", "cu_seqlens_q", "seqused_ori_kv",
              "seqused_cmp_kv", "cmp_residual_kv", "ori_topk_length")
     status = _native.library().launch_sparse_mla_plan(stream_handle(device), *(tensors[n].data_ptr() for n in names),

@@ -204,6 +204,21 @@ int launch_sparse_mla_plan(void* stream, const int32_t* cmp_sparse_indices, cons
                            const int32_t* cmp_residual_kv, const int32_t* ori_topk_length, void* workspace,
                            const SparseMlaParams* params);
 
+/* The attention over a plan alone: the persistent kernel of launch_sparse_mla
+ * (one workgroup per compute unit streaming its tokens' row lists, KV ring
+ * per params->ring) over the plan that launch_sparse_mla_plan wrote into
+ * `workspace` for the same metadata and params. The two calls together give
+ * launch_sparse_mla's output (and softmax_lse) bit for bit; the persistent
+ * kernel runs here whatever T is, and no key is split. Lets a caller time the
+ * attention kernel alone, run the plan ahead on another stream, or reuse one
+ * plan for several calls over the same selection. No counterpart in the
+ * reference, whose operator is one kernel. Returns AFA_E_SHAPE when
+ * params->debug_rows is set (the plan path writes no debug image) or no KV
+ * ring fits next to the row lists (at D = 512, WINDOW + TOPK above 3328). */
+int launch_sparse_mla_planned(void* stream, const void* q, const void* ori_kv, const void* cmp_kv,
+                              const float* sinks, void* attention_out, const void* workspace,
+                              const SparseMlaParams* params);
+
 /* Gather probe (measurement only; the counterpart of the reference's gather
  * micro-benchmark, benchmarks/attention/gather_dma.py): streams the 1 KiB rows
  * listed in a plan (D = 512, one item per token: BM = H) from ori_kv/cmp_kv

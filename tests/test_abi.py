@@ -140,6 +140,12 @@ def test_launchers_reject_null_arguments(lib):
     assert lib.launch_sparse_mla(*([None] * 15), None) == -1
     assert lib.launch_sparse_mla(*([None] * 15), ct.byref(params)) == -1
     assert lib.launch_sparse_mla_gather(*([None] * 13), ct.byref(params)) == -1
+    assert lib.launch_sparse_mla_planned(*([None] * 7), ct.byref(params)) == -1
+    assert lib.launch_sparse_mla_planned(*([None] * 7), None) == -1
+    p = ct.c_void_p(16)
+    debug = good_params(debug_rows=16)
+    assert lib.launch_sparse_mla_planned(None, p, p, p, p, p, p, ct.byref(debug)) == -2
+    assert lib.launch_sparse_mla_planned(None, p, p, p, p, p, p, ct.byref(good_params(ring=5))) == -2
     fa = _native.FaParams(B=1, HQ=8, HKV=8, D=128, dtype=1, causal=0, scale=0.088, reserved=0)
     assert lib.launch_attention_target(None, None, None, None, None, None, 8, 8, ct.byref(fa)) == -1
     p = ct.c_void_p(16)

@@ -231,6 +231,37 @@ def test_validation_cases_on_the_persistent_stream(device, case, variant, ring):
     assert_lse(lse[torch.as_tensor(tokens, device=device)], sr.oracle_lse(data, policy, tokens))
 
 
+@pytest.mark.parametrize("shape,ring", [("b8-t544", 3), ("b8-t544", 4), ("b4-t16", None)])
+def test_plan_then_planned_attention_equals_the_call(device, shape, ring):
+    """launch_sparse_mla_plan followed by launch_sparse_mla_planned (the
+    persistent kernel alone over that plan) gives sparse_mla's output and
+    softmax_lse bit for bit: at T544 (where sparse_mla itself takes the plan
+    path; each KV ring) and at T16 (where it runs the one-item kernel, whose
+    output the persistent kernel matches bit for bit when no key is split:
+    parts=1, and the planned call still runs the persistent kernel)."""
+    from ascendflow_amd.sparse_attention import sparse_mla, sparse_mla_planned
+    from ascendflow_amd.sparse_attention.probe import sparse_mla_plan
+
+    print(f"\n[sparse] plan + planned {shape} ring={ring}", flush=True)
+    b, t = (8, 544) if shape == "b8-t544" else (4, 16)
+    policy = sr.default_policy(B=b, T=t, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160)
+    data = sr.inputs(policy, "mixed")
+    tensors = to_device(data, policy, device)
+    lse = torch.full((t, policy["H"]), float("nan"), dtype=torch.float32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), softmax_lse=lse, parts=1)
+    torch.cuda.synchronize()
+    whole, whole_lse = tensors["attention_out"].clone(), lse.clone()
+    tensors["attention_out"].fill_(float("nan"))
+    lse.fill_(float("nan"))
+    workspace = sparse_mla_plan(tensors, policy)
+    sparse_mla_planned(*(tensors[k] for k in ("q", "ori_kv", "cmp_kv", "sinks", "attention_out")), workspace,
+                       **call_kwargs(policy), softmax_lse=lse, ring=ring)
+    torch.cuda.synchronize()
+    assert guard_intact(tensors), "kernel wrote past attention_out"
+    assert torch.equal(whole, tensors["attention_out"]), "plan + planned attention differs from the call"
+    assert torch.equal(whole_lse, lse), "plan + planned softmax_lse differs from the call"
+
+
 def test_relaunch_is_bitwise_deterministic(device):
     from ascendflow_amd.sparse_attention import sparse_mla
 
