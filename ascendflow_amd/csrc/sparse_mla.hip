@@ -862,8 +862,11 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   auto item_head0 = [&](int j) { return (item_key(j) % head_tiles) * a.BM; };
   const uint32_t list_base = lds_address(lists);
   auto list_address = [&](int j) { return list_base + (uint32_t)((j % LISTS) * a.list_pad) * 4u; };
+  // Selected rows of item j, at most the list capacity (a plan of other sizes
+  // cannot index past the LDS row list).
+  auto count_of = [&](int j) { return min(count_lds[j % LISTS], a.list_pad); };
   auto start = [&](Cursor& k, int j) {
-    const PartRange r = part_range(count_lds[j % LISTS], 0, 1);
+    const PartRange r = part_range(count_of(j), 0, 1);
     k.j = j;
     k.c = 0;
     k.first = r.first;
@@ -1063,7 +1066,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       // Uniform (readfirstlane): the mask below is then a scalar branch that
       // full chunks skip, not per-element selects on every chunk.
       const int live =
-          __builtin_amdgcn_readfirstlane(cur.n > 0 ? count_lds[cur.j % LISTS] - (cur.first + cur.c) * CHUNK : 0);
+          __builtin_amdgcn_readfirstlane(cur.n > 0 ? count_of(cur.j) - (cur.first + cur.c) * CHUNK : 0);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         x0[k] = s0[k];
