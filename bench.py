@@ -62,33 +62,6 @@ def time_launches(launch, steps, warmup, flush):
     return statistics.median(ms), ms, wall
 
 
-def time_after(before, launch, steps, warmup, flush):
-    """time_launches for the second of two dependent launches: each step
-    flushes the caches, runs ``before`` untimed, then brackets ``launch``
-    alone with HIP events on the same stream (median, samples in ms)."""
-    import torch
-
-    for _ in range(warmup):
-        flush()
-        before()
-        launch()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    times = []
-    for _ in range(steps):
-        flush()
-        before()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        launch()
-        end.record(stream)
-        times.append((start, end))
-    torch.cuda.synchronize()
-    ms = [s.elapsed_time(e) for s, e in times]
-    return statistics.median(ms), ms
-
-
 def warm_clocks(launch, flush, seconds=1.0):
     """Run the first workload for about `seconds` before any timing: the GPU
     otherwise reports its first launches at ramping clocks (about 10% slower).
@@ -125,28 +98,6 @@ def sparse_config(name, batch, queries, context, steps, warmup, flush, device, p
     tflops = flops / (median * 1e-3) / 1e12
     gbs = nbytes / (median * 1e-3) / 1e9
     log(f"[bench] {name}: median {median:.4f} ms, {tflops:.1f} TFLOPS, {gbs:.0f} GB/s")
-    kernels = None
-    if policy["T"] * (policy["H"] // policy["BM"]) >= 2 * 256:
-        # The call's two kernels timed apart: the plan kernel
-        # (launch_sparse_mla_plan) after the cache flush, and the persistent
-        # attention kernel (launch_sparse_mla_planned, the dominant one) alone
-        # after the flush and an untimed plan launch, as it runs in the call.
-        from ascendflow_amd.sparse_attention import sparse_mla_planned
-        from ascendflow_amd.sparse_attention.probe import sparse_mla_plan
-
-        tensors = inputs.tensors
-        workspace = sparse_mla_plan(tensors, policy)
-        plan_ms, _, _ = time_launches(lambda: sparse_mla_plan(tensors, policy, workspace), steps, warmup, flush)
-        attend = lambda: sparse_mla_planned(*(tensors[k] for k in ("q", "ori_kv", "cmp_kv", "sinks", "attention_out")),
-                                            workspace, **kwargs)
-        attn_ms, _ = time_after(lambda: sparse_mla_plan(tensors, policy, workspace), attend, steps, warmup, flush)
-        attn_tflops = flops / (attn_ms * 1e-3) / 1e12
-        kernels = {"plan_ms": round(plan_ms, 5), "attention_ms": round(attn_ms, 5),
-                   "attention_tflops": round(attn_tflops, 2),
-                   "attention_mfma_frac": round(attn_tflops / MFMA_PEAK_TFLOPS, 4)}
-        log(f"[bench] {name}: plan kernel {plan_ms:.4f} ms, attention kernel {attn_ms:.4f} ms "
-            f"({attn_tflops:.1f} TFLOPS)")
-        del workspace
     return {
         "workload": name,
         "B": batch,
@@ -162,7 +113,6 @@ def sparse_config(name, batch, queries, context, steps, warmup, flush, device, p
         "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "wall_s": round(wall, 3),
-        "kernels": kernels,
         "_inputs": inputs,
     }
 
@@ -588,10 +538,9 @@ def main():
         }
 
     bound = "hbm" if head_key == "decode" else "mfma"
-    # The dominant kernel's rate: the attention kernel timed alone where the
-    # call runs two kernels (plan + persistent attention), else the call's.
-    kernel_ms = head["kernels"]["attention_ms"] if head.get("kernels") else head["ms"]
-    achieved = head["gbs"] if bound == "hbm" else head["flops"] / (kernel_ms * 1e-3) / 1e12
+    # Over the whole call: for prefill its two kernels (the plan kernel, ~2.5%
+    # of it, and the persistent attention kernel), as launched back to back.
+    achieved = head["gbs"] if bound == "hbm" else head["tflops"]
     peak = HBM_PEAK_GBS if bound == "hbm" else MFMA_PEAK_TFLOPS
     record = {
         "metric": "sparse-MLA kernel ms + TFLOPS (prefill Q8K/32K; decode B64x6 @128K), 1 GPU",
