@@ -209,9 +209,9 @@ int launch_sparse_mla_plan(void* stream, const int32_t* cmp_sparse_indices, cons
  * per params->ring) over the plan that launch_sparse_mla_plan wrote into
  * `workspace` for the same metadata and params. The two calls together give
  * launch_sparse_mla's output (and softmax_lse) bit for bit; the persistent
- * kernel runs here whatever T is, and no key is split. Lets a caller time the
- * attention kernel alone, run the plan ahead on another stream, or reuse one
- * plan for several calls over the same selection. No counterpart in the
+ * kernel runs here whatever T is, and no key is split. Lets a caller run the
+ * plan ahead on another stream or reuse one plan for several calls over the
+ * same selection. No counterpart in the
  * reference, whose operator is one kernel. Returns AFA_E_SHAPE when
  * params->debug_rows is set (the plan path writes no debug image) or no KV
  * ring fits next to the row lists (at D = 512, WINDOW + TOPK above 3328). */
