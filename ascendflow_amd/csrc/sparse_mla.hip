@@ -481,7 +481,6 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       }
     }
   };
-  constexpr int Q_LOADS_PER_WAVE = (Q_LOADS + NW - 1) / NW;
   __shared__ int request_scratch[NW];
   int n_rows;
   {
