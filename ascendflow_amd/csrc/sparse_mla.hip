@@ -815,7 +815,7 @@ struct Cursor {
 //    score-wave KV fetch would wait for them);
 //  - each item's running max starts at its sinks (one lane group counts the
 //    sink's e^(sink - m)), its output accumulators are cleared on its first PV
-//    step, and its running max and denominator travel through LDS slot item & 1.
+//    step, and its denominator travels through LDS slot item & 1.
 // The first item's Q goes through LDS as in sparse_mla_kernel.
 template <int DT, int D, int NQ, int NP, int NS>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(SparseArgs a) {
@@ -843,7 +843,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
   __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][NQ][64];
   __shared__ float alpha_lds[2][BMH];
   __shared__ __attribute__((aligned(16))) int flag_lds[2][4];
-  __shared__ float ml_lds[2][2][BMH];  // item parity: running max (log2 units), denominator
+  __shared__ float l_lds[2][BMH];  // item parity: softmax denominator per head
   __shared__ __attribute__((aligned(16))) int count_lds[LISTS];
   extern __shared__ __attribute__((aligned(16))) uint32_t lists[];  // [LISTS][list_pad]
 
@@ -1109,8 +1109,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       if (cur.c == cur.chunks() - 1) {
         const float l = sum_over_lane_groups(l_run);
         if (g == 0) {
-          ml_lds[cur.j & 1][0][16 * wave + i16] = m_run;
-          ml_lds[cur.j & 1][1][16 * wave + i16] = l;
+          l_lds[cur.j & 1][16 * wave + i16] = l;
           if (a.lse != nullptr)
             a.lse[(size_t)item_token(cur.j) * a.H + item_head0(cur.j) + 16 * wave + i16] = lse_of(m_run, l);
         }
@@ -1146,7 +1145,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
       for (int ht = 0; ht < NQ; ++ht) {
-        const float inv = 1.0f / ml_lds[par][1][16 * ht + i16];
+        const float inv = 1.0f / l_lds[par][16 * ht + i16];
         store_head_tile<DT, DPV, ROW_BYTES, 15>(tile, (uint32_t)(dbase / 8), o[ht], inv, out0 + (size_t)16 * ht * D,
                                                 D, lane);
       }
