@@ -96,6 +96,12 @@ __device__ __forceinline__ int swz(int row, int unit) { return unit ^ (row & 15)
 // transposing read take the rows {0,2,4,6}, {8,10,12,14}, {9,11,13,15}, {1,3,5,7}.
 __device__ __forceinline__ int sigma(int m) { return ((m & 3) << 1) + ((0x1980 >> ((m >> 2) << 2)) & 15); }
 
+// Load-to-LDS (global_load_lds_*): the LDS destination is M0, set by an
+// s_mov_b32 in the same asm statement. GFX9 needs one wait state between an
+// SALU write of M0 and an LDS-DMA instruction that reads it; the compiler
+// inserts it for its own code but cannot see inside inline asm, so every such
+// statement here carries its own s_nop 0 between the two.
+
 // LDS byte address of a __shared__ object, and an LDS pointer from one.
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const AFA_LDS void*)p;
@@ -124,9 +130,10 @@ __device__ __forceinline__ uint32_t opaque_uniform(uint32_t v) {
 // expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14, all other fields at max).
 constexpr int WAIT_LGKM0 = 0xC07F;
 // s_waitcnt vmcnt(N) alone: wait until at most N vector memory operations of
-// this wave are in flight. The counter retires loads, loads to LDS and stores
-// of a wave in issue order (the compiler's own waits behind a mix of loads and
-// stores assume the same), so this waits for all but the N most recent.
+// this wave are in flight. The kernels use N > 0 only where every operation in
+// flight is a load (loads and loads to LDS retire in issue order, so this waits
+// for all but the N most recent); behind stores they wait with N = 0, since
+// stores are not relied on to retire in order with loads.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");

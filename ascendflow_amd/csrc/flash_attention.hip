@@ -147,9 +147,9 @@ __global__ __launch_bounds__(NW * 64) void fa_forward_kernel(FaArgs a) {
       }
       const uint32_t row0 = (uint32_t)((wave * LOADS + p) * ROWS_PER_LOAD * ROW_BYTES);
       const uint32_t kd = tile_address(chunk, 0) + row0, vd = tile_address(chunk, 1) + row0;
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+      __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                        :: "s"(kd), "v"(off), "s"(kbase) : "memory");
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+      __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                        :: "s"(vd), "v"(off), "s"(vbase) : "memory");
     }
   };

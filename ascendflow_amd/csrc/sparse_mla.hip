@@ -476,7 +476,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
         const int pos = k * 64 + lane;  // 16-byte unit position in the tile
         const int r = pos / UNITS, u = pos % UNITS;
         const uint32_t off = (uint32_t)(r * ROW_BYTES + ((u ^ (r & 15)) << 4));
-        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                          :: "s"(q_lds + (uint32_t)k * 1024u), "v"(off), "s"(q_src) : "memory");
       }
     }
@@ -553,7 +553,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
         const uint32_t e = __builtin_amdgcn_readfirstlane(entry_next[p]);
         const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES;
         const uint32_t dst = tile + (uint32_t)(r * ROW_BYTES);
-        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                          :: "s"(dst), "v"(unit_offset[p]), "s"(row) : "memory");
       }
       if (chunk + 1 < chunks) read_entries(chunk + 1);
@@ -565,7 +565,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
         const uint32_t e = row_list[list_chunk(chunk) * CHUNK + r];
         const char* src = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES + ((upos ^ (r & 15)) << 4);
         const uint32_t dst = tile + (uint32_t)((wave * 64 + p * NT) * 16);
-        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                          :: "s"(dst), "v"(src) : "memory");
       }
     }
@@ -817,7 +817,7 @@ struct Cursor {
 //    sink's e^(sink - m)), its output accumulators are cleared on its first PV
 //    step, and its denominator travels through LDS slot item & 1.
 // The first item's Q goes through LDS as in sparse_mla_kernel.
-template <int DT, int D, int NQ, int NP, int NS>
+template <int DT, int D, int NQ, int NP, int NS, bool CLAMP>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
@@ -887,10 +887,10 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
     const uint32_t* src = a.plan_rows + (size_t)token * a.list_pad;
     const uint32_t dst = list_address(j);
     if (wave == NQ && lane == 0)
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2"
+      __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                        :: "s"(lds_address(&count_lds[j % LISTS])), "v"(0u), "s"(a.plan_count + token) : "memory");
     for (int u = wave - NQ; u < a.list_pad / 256; u += NP)
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+      __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                        :: "s"(dst + (uint32_t)u * 1024u), "v"((uint32_t)lane * 16u), "s"(src + u * 256) : "memory");
   };
 
@@ -910,7 +910,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       const int pos = k * 64 + lane;
       const int r = pos / UNITS, u = pos % UNITS;
       const uint32_t off = (uint32_t)(r * ROW_BYTES + ((u ^ (r & 15)) << 4));
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+      __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                        :: "s"(q_lds + (uint32_t)k * 1024u), "v"(off), "s"(q_src) : "memory");
     }
   }
@@ -937,6 +937,18 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
 #pragma unroll
     for (int p = 0; p < PIECES; ++p) entry_next[p] = l[k.list_chunk() * CHUNK + ow * PIECES + p];
   };
+  // CLAMP (the planned entry point, whose plan is a workspace the caller
+  // hands over): each row is clamped to its cache, so an entry that is not
+  // from a plan of these sizes reads a wrong row, never memory outside the
+  // caches. Plans written by this library's plan kernel need no clamp (two
+  // more scalar operations per row cost ~3.5% on prefill).
+  const uint32_t ori_last = (uint32_t)(a.ori_blocks * a.PAGE - 1);
+  const uint32_t cmp_last = (uint32_t)(a.cmp_blocks * (a.PAGE / a.RATIO) - 1);
+  auto row_of = [&](uint32_t e) {
+    const bool c = (e & CMP_BIT) != 0u;
+    const uint32_t r = e & ~CMP_BIT;
+    return (c ? cmp : ori) + (size_t)(CLAMP ? min(r, c ? cmp_last : ori_last) : r) * ROW_BYTES;
+  };
   // The chunk at cursor k into ring tile s % NS (ROW_LOADS: entries already read).
   auto fetch = [&](int s, const Cursor& k) {
     const uint32_t tile = tile_address(s);
@@ -945,8 +957,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
       for (int p = 0; p < PIECES; ++p) {
         const int r = ow * PIECES + p;
         const uint32_t e = __builtin_amdgcn_readfirstlane(entry_next[p]);
-        const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES;
-        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+        const char* row = row_of(e);
+        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                          :: "s"(tile + (uint32_t)(r * ROW_BYTES)), "v"(unit_offset[p]), "s"(row) : "memory");
       }
     } else {
@@ -957,8 +969,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
         const int flat = otid + p * NO;
         const int r = flat / UNITS, upos = flat % UNITS;
         const uint32_t e = l[k.list_chunk() * CHUNK + r];
-        const char* src = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES + ((upos ^ (r & 15)) << 4);
-        __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+        const char* src = row_of(e) + ((upos ^ (r & 15)) << 4);
+        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                          :: "s"(tile + (uint32_t)((ow * 64 + p * NO) * 16)), "v"(src) : "memory");
       }
     }
@@ -1157,10 +1169,9 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
     for (int s = 0;; ++s) {
       const bool score_active = cur.j < J;
       if (!score_active && !ovalid) break;
-      // KV(s) has landed once at most the younger fetch batch is in flight.
-      // After output stores, wait for those too: the counter retires in issue
-      // order, so waiting for KV(s) alone would do, but letting the stores run
-      // on into the next step measured ~2% slower on prefill.
+      // KV(s) has landed once at most the younger fetch batch is in flight
+      // (only loads are in flight then). After output stores the wait is for
+      // everything (vmcnt(0)): a partial wait is never taken behind stores.
       if (stored || !ahead_loaded)
         wait_vmcnt<0>();
       else
@@ -1377,7 +1388,7 @@ __global__ __launch_bounds__(256) void gather_probe_kernel(const char* ori, cons
   // Lists of all items to LDS, one round trip.
   for (int j = 0; j < J; ++j)
     for (int u = wave; u < list_pad / 256; u += 4)
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+      __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                        :: "s"(lds_address(probe_lists) + (uint32_t)(j * list_pad + u * 256) * 4u),
                           "v"((uint32_t)lane * 16u), "s"(lists + (size_t)item[j] * list_pad + u * 256) : "memory");
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1399,7 +1410,7 @@ __global__ __launch_bounds__(256) void gather_probe_kernel(const char* ori, cons
       const int r = wave * PER_WAVE + p;
       const uint32_t e = __builtin_amdgcn_readfirstlane(probe_lists[j * list_pad + c * PROBE_ROWS + r]);
       const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW;
-      __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+      __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                        :: "s"(tile + (uint32_t)(r * ROW)), "v"((uint32_t)((lane ^ (r & 15)) << 4)), "s"(row) : "memory");
     }
   };
@@ -1607,23 +1618,23 @@ static int device_cus() {
 template <int DT, int D, int NQ, int NP>
 static int persistent_ring(const SparseArgs& a) {
   const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
-  if (a.ring == 4 && fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>>(5 * lds) == AFA_OK) return 4;
-  return fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>>(4 * lds) == AFA_OK ? 3 : 0;
+  if (a.ring == 4 && fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 4, false>>(5 * lds) == AFA_OK) return 4;
+  return fits_lds<sparse_mla_persistent_kernel<DT, D, NQ, NP, 3, false>>(4 * lds) == AFA_OK ? 3 : 0;
 }
 
 // The persistent kernel over the plan at a.plan_count / a.plan_rows: one
 // workgroup per CU (at most one per item).
-template <int DT, int D, int NQ, int NP>
+template <int DT, int D, int NQ, int NP, bool CLAMP = false>
 static int launch_persistent(const SparseArgs& a, int ring, hipStream_t stream) {
   const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
   static const int cus = device_cus();
   const int64_t items = (int64_t)a.T * (a.H / a.BM);
   const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
   if (ring == 4)
-    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4>), dim3(grid), dim3((NQ + NP) * 64), 5 * lds,
+    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4, CLAMP>), dim3(grid), dim3((NQ + NP) * 64), 5 * lds,
                        stream, a);
   else
-    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3>), dim3(grid), dim3((NQ + NP) * 64), 4 * lds,
+    hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3, CLAMP>), dim3(grid), dim3((NQ + NP) * 64), 4 * lds,
                        stream, a);
   return (int)hipGetLastError();
 }
@@ -1829,14 +1840,14 @@ static int dispatch_planned(const SparseArgs& a, hipStream_t s) {
   const bool four = a.BM == 64;
   switch (a.D) {
     case 128:
-      return four ? run(persistent_ring<DT, 128, 4, 4>, launch_persistent<DT, 128, 4, 4>)
-                  : run(persistent_ring<DT, 128, 2, 2>, launch_persistent<DT, 128, 2, 2>);
+      return four ? run(persistent_ring<DT, 128, 4, 4>, launch_persistent<DT, 128, 4, 4, true>)
+                  : run(persistent_ring<DT, 128, 2, 2>, launch_persistent<DT, 128, 2, 2, true>);
     case 256:
-      return four ? run(persistent_ring<DT, 256, 4, 4>, launch_persistent<DT, 256, 4, 4>)
-                  : run(persistent_ring<DT, 256, 2, 2>, launch_persistent<DT, 256, 2, 2>);
+      return four ? run(persistent_ring<DT, 256, 4, 4>, launch_persistent<DT, 256, 4, 4, true>)
+                  : run(persistent_ring<DT, 256, 2, 2>, launch_persistent<DT, 256, 2, 2, true>);
     default:
-      return four ? run(persistent_ring<DT, 512, 4, 4>, launch_persistent<DT, 512, 4, 4>)
-                  : run(persistent_ring<DT, 512, 2, 2>, launch_persistent<DT, 512, 2, 2>);
+      return four ? run(persistent_ring<DT, 512, 4, 4>, launch_persistent<DT, 512, 4, 4, true>)
+                  : run(persistent_ring<DT, 512, 2, 2>, launch_persistent<DT, 512, 2, 2, true>);
   }
 }
 

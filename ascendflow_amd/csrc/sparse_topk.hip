@@ -387,7 +387,10 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
                             : min(samples, (int)((2 * (int64_t)take * samples) / cand) + 16);
   int too_few = 0, too_many = samples + 1, n = 0;
   bool buffered = false;
-  for (int round = 0; round < TK_FILTER_ROUNDS; ++round) {
+  // A filter pass succeeds only when take <= n <= CAP: with take above the
+  // buffer's capacity no pass can, so the row goes straight to the whole-row
+  // selection below instead of being streamed by every filter round first.
+  for (int round = 0; take <= CAP && round < TK_FILTER_ROUNDS; ++round) {
     const uint32_t estimate = radix_select<THREADS>(
         [&](auto f) {
 #pragma unroll

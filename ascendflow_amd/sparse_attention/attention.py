@@ -16,10 +16,13 @@ they do not change the gfx950 schedule.
 from __future__ import annotations
 
 import ctypes as ct
+import functools
+from collections import OrderedDict
 
 import torch
 
 from .. import _native
+from .._native import SparseMlaParams
 from .._tensors import DTYPES, check_disjoint, check_tensor, require, storage_dtype, stream_handle
 
 
@@ -91,7 +94,87 @@ def check_inputs(tensors, *, B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_B
     return device
 
 
-def sparse_mla(
+TENSOR_NAMES = ("q", "ori_kv", "cmp_kv", "cmp_sparse_indices", "ori_block_table", "cmp_block_table", "cu_seqlens_q",
+                "seqused_ori_kv", "seqused_cmp_kv", "cmp_residual_kv", "ori_topk_length", "sinks", "attention_out")
+
+
+class Binding:
+    """Launch state of one (device, stream, sizes) key, built and validated
+    once: the launcher parameters, the workspace size and a reusable
+    workspace. The counterpart of the reference runtime's ``KernelLaunch``,
+    kept per (stream, runtime sizes) with its workspace allocated once
+    (``src/runtime/torch.py:170-186``, ``src/runtime/kernel.py:39-50``).
+
+    A later call with the same key checks each tensor's shape, dtype,
+    contiguity and device in one pass and repeats the pairwise disjointness
+    check only when a pointer differs from the last validated call."""
+
+    __slots__ = ("device", "stream", "specs", "params", "params_ref", "nbytes", "workspace", "validated")
+
+    def __init__(self, device, stream, specs, params, nbytes):
+        self.device = device
+        self.stream = stream
+        self.specs = specs
+        self.params = params
+        self.params_ref = ct.pointer(params)
+        self.nbytes = nbytes
+        self.workspace = None
+        self.validated = None
+
+
+MAX_BINDINGS = 16
+_bindings: "OrderedDict[tuple, Binding]" = OrderedDict()
+
+
+def release_bindings():
+    """Drops every cached binding and the workspaces they hold."""
+    _bindings.clear()
+
+
+def binding_key(device_index, stream, sizes):
+    return (device_index, stream) + sizes
+
+
+def _binding(device, stream, sizes, policy, dtype, parts, ring):
+    key = binding_key(device.index, stream, sizes)
+    b = _bindings.get(key)
+    if b is not None:
+        _bindings.move_to_end(key)
+        return b
+    B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, SCALE = policy
+    b16 = DTYPES[dtype]
+    i32 = torch.int32
+    width = MAX_SEQ // PAGE
+    shapes = ((T, H, D), (ORI_BLOCKS, PAGE, 1, D), (CMP_BLOCKS, PAGE // RATIO, 1, D), (T, 1, TOPK), (B, width),
+              (B, width), (B + 1,), (B,), (B,), (B,), (T, 1), (H,), (T, H, D))
+    dtypes = (b16, b16, b16, i32, i32, i32, i32, i32, i32, i32, i32, torch.float32, b16)
+    specs = tuple((name, torch.Size(shape), dt) for name, shape, dt in zip(TENSOR_NAMES, shapes, dtypes))
+    params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE,
+                         None, parts, None, ring)
+    nbytes = ct.c_uint64(0)
+    _native.check(_native.library().workspace_size_sparse_mla(ct.byref(nbytes), ct.byref(params)),
+                  "workspace_size_sparse_mla")
+    b = Binding(device, stream, specs, params, int(nbytes.value))
+    _bindings[key] = b
+    while len(_bindings) > MAX_BINDINGS:
+        _bindings.popitem(last=False)
+    return b
+
+
+def _pointers(b, tensors):
+    """Data pointers of the 13 operands after the per-call checks; any failure
+    is reported by the full check (same messages as the first call)."""
+    ptrs = []
+    index = b.device.index
+    for (name, shape, dt), t in zip(b.specs, tensors):
+        if (not isinstance(t, torch.Tensor) or t.dtype is not dt or t.shape != shape or not t.is_contiguous()
+                or t.get_device() != index):
+            check_tensor(name, t, shape, dt, b.device)
+        ptrs.append(t.data_ptr())
+    return ptrs
+
+
+def _prepare(
     q,
     ori_kv,
     cmp_kv,
@@ -133,6 +216,72 @@ def sparse_mla(
     workspace=None,
     ring=None,
 ):
+    """Validates one call and returns its launch state (see ``sparse_mla``)."""
+    dtype = storage_dtype(DTYPE)
+    tensors = (q, ori_kv, cmp_kv, cmp_sparse_indices, ori_block_table, cmp_block_table, cu_seqlens_q, seqused_ori_kv,
+               seqused_cmp_kv, cmp_residual_kv, ori_topk_length, sinks, attention_out)
+    device_index = q.get_device() if isinstance(q, torch.Tensor) else -1
+    if device_index < 0:
+        check_tensor("q", q, (T, H, D), DTYPES[dtype])  # raises: not a device tensor
+    stream = torch._C._cuda_getCurrentRawStream(device_index)
+    sizes = (B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, ROWS, S, BM, PARTS, GROUPS, VR,
+             BK, C, dtype, SCALE, parts, ring)
+    b = _bindings.get(binding_key(device_index, stream, sizes))
+    if b is None:
+        check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PARTS, GROUPS, VR, BK, C, SCALE)
+        require(parts is None or parts in range(1, 9), "parts must be None or 1..8")
+        require(ring in (None, 3, 4), "ring must be None, 3 or 4")
+        check_inputs(
+            dict(zip(TENSOR_NAMES, tensors)), B=B, T=T, H=H, D=D, PAGE=PAGE, RATIO=RATIO, MAX_SEQ=MAX_SEQ,
+            ORI_BLOCKS=ORI_BLOCKS, CMP_BLOCKS=CMP_BLOCKS, TOPK=TOPK, dtype=dtype,
+        )
+        b = _binding(q.device, stream, sizes,
+                     (B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, SCALE),
+                     dtype, parts or 0, ring or 0)
+    ptrs = _pointers(b, tensors)
+    params_ref = b.params_ref
+    extra = ()
+    if debug_rows is not None or softmax_lse is not None:
+        # Per-call output pointers go into a copy, so the binding's parameters stay shared.
+        params = SparseMlaParams.from_buffer_copy(b.params)
+        if debug_rows is not None:
+            check_tensor("debug_rows", debug_rows, (T, S, 2), torch.int32, b.device)
+            params.debug_rows = debug_rows.data_ptr()
+            extra += (("debug_rows", debug_rows),)
+        if softmax_lse is not None:
+            check_tensor("softmax_lse", softmax_lse, (T, H), torch.float32, b.device)
+            params.softmax_lse = softmax_lse.data_ptr()
+            extra += (("softmax_lse", softmax_lse),)
+        params_ref = ct.pointer(params)
+    own_workspace = workspace is None
+    if workspace is not None:
+        require(isinstance(workspace, torch.Tensor) and workspace.dtype == torch.uint8 and workspace.is_contiguous()
+                and workspace.device == b.device, "workspace must be a contiguous uint8 tensor on the operands' device")
+        require(workspace.numel() >= b.nbytes, f"workspace holds {workspace.numel()} bytes, needs {b.nbytes}")
+        extra += (("workspace", workspace),)
+    elif b.nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            workspace = torch.empty(b.nbytes, dtype=torch.uint8, device=b.device)
+        else:
+            if b.workspace is None:
+                b.workspace = torch.empty(b.nbytes, dtype=torch.uint8, device=b.device)
+            workspace = b.workspace
+    ws_ptr = None if workspace is None else workspace.data_ptr()
+    signature = (*ptrs, ws_ptr, *((name, t.data_ptr(), t.numel()) for name, t in extra))
+    if signature != b.validated:
+        # Written operands (the output, the workspace, softmax_lse, the debug
+        # image) must not overlap any other operand.
+        named = [(name, t, name == "attention_out") for name, t in zip(TENSOR_NAMES, tensors)]
+        named += [(name, t, True) for name, t in extra]
+        if own_workspace and workspace is not None:
+            named.append(("workspace", workspace, True))
+        check_disjoint(named)
+        b.validated = signature
+    return device_index, stream, ptrs, ws_ptr, params_ref, workspace, attention_out
+
+
+@functools.wraps(_prepare, assigned=("__module__",))
+def sparse_mla(*args, **kwargs):
     """Sparse MLA forward; writes ``attention_out`` [T, H, D] and returns it.
 
     ``debug_rows`` (optional int32 [T, S, 2] device tensor) receives, per
@@ -160,63 +309,47 @@ def sparse_mla(
     does not depend on it.
 
     ``workspace`` (optional uint8 device tensor of at least
-    ``workspace_bytes(...)`` bytes) replaces the per-call allocation. When
+    ``workspace_bytes(...)`` bytes) replaces the binding's own workspace. When
     the plan path runs (at least two work items per CU, no split, no debug
     image), it holds the row-list plan afterwards (``plan_layout``): the
     selected-row count of every token, then every token's list of tagged
     rows (bit 31 set for cmp_kv) padded with its first row to whole 32-row
     chunks (32 entries of ori_kv row 0 for an empty selection).
+
+    Without ``workspace``, each (device, stream, sizes) binding keeps one
+    workspace and reuses it for every call on that stream (calls on one
+    stream run in order); under HIP graph capture the call allocates its own
+    from the graph's pool instead. ``release_bindings()`` frees them.
     """
-    dtype = storage_dtype(DTYPE)
-    check_policy(B, T, H, D, PAGE, RATIO, MAX_SEQ, WINDOW, TOPK, ROWS, S, BM, PARTS, GROUPS, VR, BK, C, SCALE)
-    tensors = {
-        "q": q,
-        "ori_kv": ori_kv,
-        "cmp_kv": cmp_kv,
-        "cmp_sparse_indices": cmp_sparse_indices,
-        "ori_block_table": ori_block_table,
-        "cmp_block_table": cmp_block_table,
-        "cu_seqlens_q": cu_seqlens_q,
-        "seqused_ori_kv": seqused_ori_kv,
-        "seqused_cmp_kv": seqused_cmp_kv,
-        "cmp_residual_kv": cmp_residual_kv,
-        "ori_topk_length": ori_topk_length,
-        "sinks": sinks,
-        "attention_out": attention_out,
-    }
-    device = check_inputs(
-        tensors, B=B, T=T, H=H, D=D, PAGE=PAGE, RATIO=RATIO, MAX_SEQ=MAX_SEQ,
-        ORI_BLOCKS=ORI_BLOCKS, CMP_BLOCKS=CMP_BLOCKS, TOPK=TOPK, dtype=dtype,
-    )
-    if debug_rows is not None:
-        check_tensor("debug_rows", debug_rows, (T, S, 2), torch.int32, device)
-    if softmax_lse is not None:
-        check_tensor("softmax_lse", softmax_lse, (T, H), torch.float32, device)
-        check_disjoint([(name, t, False) for name, t in tensors.items()] + [("softmax_lse", softmax_lse, True)])
-    require(parts is None or parts in range(1, 9), "parts must be None or 1..8")
-    require(ring in (None, 3, 4), "ring must be None, 3 or 4")
-    params = make_params(B, T, H, D, PAGE, RATIO, MAX_SEQ, ORI_BLOCKS, CMP_BLOCKS, WINDOW, TOPK, S, BM, dtype, SCALE, debug_rows,
-                         parts or 0, softmax_lse, ring or 0)
+    _, stream, ptrs, ws_ptr, params_ref, _, out = _prepare(*args, **kwargs)
+    _native.check(_native.library().launch_sparse_mla(stream, *ptrs, ws_ptr, params_ref), "launch_sparse_mla")
+    return out
+
+
+def bind(*args, **kwargs):
+    """Validates a ``sparse_mla`` call once and returns ``invoke()``, which
+    launches it again on the current stream with no further checks (the
+    reference's ``TensorKernel.bind``, ``src/runtime/torch.py:94-190``: bound
+    tensors must keep their shape, dtype and storage). A stream other than the
+    one current at bind time gets its own binding and workspace, as
+    concurrent streams need separate bindings (``src/runtime/kernel.py:10``)."""
+    device_index, stream0, ptrs, ws_ptr, params_ref, workspace, out = _prepare(*args, **kwargs)
     lib = _native.library()
-    # The workspace holds the per-token row-list plan (see workspace_size_sparse_mla);
-    # the caching allocator hands it out in stream order, so no host sync.
-    nbytes = ct.c_uint64(0)
-    _native.check(lib.workspace_size_sparse_mla(ct.byref(nbytes), ct.byref(params)), "workspace_size_sparse_mla")
-    if workspace is None:
-        workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=device) if nbytes.value else None
-    else:
-        require(isinstance(workspace, torch.Tensor) and workspace.dtype == torch.uint8 and workspace.is_contiguous()
-                and workspace.device == device, "workspace must be a contiguous uint8 tensor on the operands' device")
-        require(workspace.numel() >= nbytes.value, f"workspace holds {workspace.numel()} bytes, needs {nbytes.value}")
-        check_disjoint([(name, t, False) for name, t in tensors.items()] + [("workspace", workspace, True)])
-    status = lib.launch_sparse_mla(
-        stream_handle(device),
-        *(tensors[name].data_ptr() for name in tensors),
-        None if workspace is None else workspace.data_ptr(),
-        ct.byref(params),
-    )
-    _native.check(status, "launch_sparse_mla")
-    return attention_out
+    held = {stream0: (ptrs, ws_ptr, params_ref, workspace)}
+
+    def invoke():
+        stream = torch._C._cuda_getCurrentRawStream(device_index)
+        state = held.get(stream)
+        if state is None:
+            _, _, p, w, r, ws, _ = _prepare(*args, **kwargs)
+            state = held[stream] = (p, w, r, ws)
+        _native.check(lib.launch_sparse_mla(stream, *state[0], state[1], state[2]), "launch_sparse_mla")
+        return out
+
+    return invoke
+
+
+sparse_mla.bind = bind
 
 
 def sparse_mla_planned(q, ori_kv, cmp_kv, sinks, attention_out, workspace, B, T, H=64, D=512, PAGE=128, RATIO=2,
@@ -224,9 +357,13 @@ def sparse_mla_planned(q, ori_kv, cmp_kv, sinks, attention_out, workspace, B, T,
                        SCALE=0.04419417382415922, *, softmax_lse=None, ring=None):
     """The attention over a row-list plan alone (``launch_sparse_mla_planned``).
 
-    ``workspace`` holds the plan of the same metadata, written by
-    ``launch_sparse_mla_plan`` (``probe.sparse_mla_plan``) or by a plain
-    ``sparse_mla`` call that took the plan path (``plan_layout``). Writes
+    ``workspace`` holds the plan of the same metadata and sizes, written by
+    ``launch_sparse_mla_plan`` (``probe.sparse_mla_plan``; layout
+    ``plan_layout``). Whether a plain ``sparse_mla`` call wrote a plan into its
+    workspace depends on the device and the split, so that is not a plan to
+    rely on; the kernel clamps every count and row id it reads to the list
+    capacity and the caches, so a foreign workspace gives a wrong output, not
+    a read outside ``ori_kv``/``cmp_kv``. Writes
     ``attention_out`` (and ``softmax_lse``) exactly as ``sparse_mla`` does on
     the same inputs, with the persistent kernel whatever ``T`` is, and returns
     it. ``ring`` as in ``sparse_mla``.

@@ -78,6 +78,24 @@ def warm_clocks(launch, flush, seconds=1.0):
         torch.cuda.synchronize()
 
 
+def host_times(launch, flush, calls=30):
+    """Median and max host time in microseconds of one call (the Python entry
+    and the launcher, no synchronisation), each call queued behind the cache
+    flush so that it never waits for the GPU."""
+    import torch
+
+    times = []
+    for k in range(calls):
+        flush()
+        t0 = time.perf_counter()
+        launch()
+        times.append((time.perf_counter() - t0) * 1e6)
+        if k % 10 == 9:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return round(statistics.median(times), 1), round(max(times), 1)
+
+
 def sparse_config(name, batch, queries, context, steps, warmup, flush, device, prewarm=0.0):
     import torch
 
@@ -97,7 +115,13 @@ def sparse_config(name, batch, queries, context, steps, warmup, flush, device, p
     nbytes = compulsory_bytes(policy, inputs.touched)
     tflops = flops / (median * 1e-3) / 1e12
     gbs = nbytes / (median * 1e-3) / 1e9
-    log(f"[bench] {name}: median {median:.4f} ms, {tflops:.1f} TFLOPS, {gbs:.0f} GB/s")
+    # The reference's secondary figure: selected KV logical bytes, valid rows x
+    # D x 2 over every query (sparse_performance.py:273-275), i.e. flops / (2 H).
+    logical = flops // (2 * policy["H"])
+    host_us, host_max = host_times(lambda: sparse_mla(*args, **kwargs), flush)
+    bound_us, bound_max = host_times(sparse_mla.bind(*args, **kwargs), flush)
+    log(f"[bench] {name}: median {median:.4f} ms, {tflops:.1f} TFLOPS, {gbs:.0f} GB/s; host per call {host_us} us "
+        f"(bound {bound_us} us)")
     return {
         "workload": name,
         "B": batch,
@@ -112,6 +136,12 @@ def sparse_config(name, batch, queries, context, steps, warmup, flush, device, p
         "gbs": round(gbs, 1),
         "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "logical_kv_bytes": logical,
+        "logical_kv_gbs": round(logical / (median * 1e-3) / 1e9, 1),
+        "host_us": host_us,
+        "host_us_max": host_max,
+        "host_us_bound": bound_us,
+        "host_us_bound_max": bound_max,
         "wall_s": round(wall, 3),
         "_inputs": inputs,
     }

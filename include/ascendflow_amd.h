@@ -211,7 +211,12 @@ int launch_sparse_mla_plan(void* stream, const int32_t* cmp_sparse_indices, cons
  * launch_sparse_mla's output (and softmax_lse) bit for bit; the persistent
  * kernel runs here whatever T is, and no key is split. Lets a caller run the
  * plan ahead on another stream or reuse one plan for several calls over the
- * same selection. No counterpart in the
+ * same selection. The plan must come from launch_sparse_mla_plan with the
+ * same metadata and params (whether a launch_sparse_mla call wrote one depends
+ * on the device and the split, so its workspace is not a plan to rely on).
+ * Counts and row ids read from `workspace` are clamped to the list capacity
+ * and to ori_kv / cmp_kv, so a workspace holding anything else gives a wrong
+ * output but no access outside the caches. No counterpart in the
  * reference, whose operator is one kernel. Returns AFA_E_SHAPE when
  * params->debug_rows is set (the plan path writes no debug image) or no KV
  * ring fits next to the row lists (at D = 512, WINDOW + TOPK above 3328). */
@@ -259,8 +264,9 @@ int launch_sparse_topk_indices(void* stream, const float* scores, const int32_t*
 
 /* Measurement helpers (no reference kernel; the reference sweeps a >= 4x L2
  * buffer before each timed launch, benchmarks/cache.py:13-92 and
- * benchmarks/cache_sweep.py:15-32). Streams `bytes` of `buffer` through the
- * caches with a read-modify-write so the next launch starts cold. */
+ * benchmarks/cache_sweep.py:15-32). Reads `bytes` of `buffer` through the
+ * caches (cached 16-byte loads, nothing written back for a zero-filled
+ * buffer) so that the next launch starts cold. */
 int launch_cache_flush(void* stream, void* buffer, uint64_t bytes);
 
 /* Measurement helper (no reference kernel): runs `spins` dependent FMAs in

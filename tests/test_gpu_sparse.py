@@ -276,6 +276,76 @@ def test_relaunch_is_bitwise_deterministic(device):
     assert torch.equal(first, tensors["attention_out"])
 
 
+def test_binding_reuse_bind_and_streams_give_the_same_output(device):
+    """The per-(device, stream, sizes) binding: a first call builds it, later
+    calls reuse its parameters and workspace; ``sparse_mla.bind`` validates
+    once and relaunches; another stream gets its own binding. On the plan +
+    persistent path (T = 544 over 8 requests) every variant must give the
+    first call's output and softmax_lse bit for bit."""
+    from ascendflow_amd.sparse_attention import attention as A
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    A.release_bindings()
+    policy = sr.default_policy(B=8, T=544, MAX_SEQ=4096, ORI_BLOCKS=256, CMP_BLOCKS=256)
+    data = sr.inputs(policy, "mixed")
+    tensors = to_device(data, policy, device)
+    lse = torch.empty((policy["T"], policy["H"]), dtype=torch.float32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), softmax_lse=lse)
+    torch.cuda.synchronize()
+    first, first_lse = tensors["attention_out"].clone(), lse.clone()
+    assert len(A._bindings) == 1
+    binding = next(iter(A._bindings.values()))
+    assert binding.workspace is not None and binding.workspace.numel() == binding.nbytes
+    for _ in range(2):
+        tensors["attention_out"].zero_()
+        sparse_mla(*call_args(tensors), **call_kwargs(policy), softmax_lse=lse)
+    torch.cuda.synchronize()
+    assert len(A._bindings) == 1
+    assert torch.equal(first, tensors["attention_out"]) and torch.equal(first_lse, lse)
+    invoke = sparse_mla.bind(*call_args(tensors), **call_kwargs(policy), softmax_lse=lse)
+    tensors["attention_out"].zero_()
+    lse.zero_()
+    invoke()
+    torch.cuda.synchronize()
+    assert torch.equal(first, tensors["attention_out"]) and torch.equal(first_lse, lse)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        tensors["attention_out"].zero_()
+        invoke()
+        sparse_mla(*call_args(tensors), **call_kwargs(policy))
+    torch.cuda.synchronize()
+    assert len(A._bindings) == 2  # one more binding: the side stream's (its bound and plain calls share it)
+    assert torch.equal(first, tensors["attention_out"])
+    assert guard_intact(tensors), "kernel wrote past attention_out"
+    A.release_bindings()
+
+
+def test_written_operands_must_not_overlap_the_workspace(device):
+    """softmax_lse or the debug image carved out of the caller's workspace is
+    rejected before any launch (the plan would otherwise overwrite them, or
+    they the plan)."""
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    policy = sr.default_policy(B=8, T=544, MAX_SEQ=4096, ORI_BLOCKS=256, CMP_BLOCKS=256)
+    tensors = to_device(sr.inputs(policy, "mixed"), policy, device)
+    workspace = workspace_for(policy, device)
+    lse = workspace[: policy["T"] * policy["H"] * 4].view(torch.float32).view(policy["T"], policy["H"])
+    with pytest.raises(ValueError, match="overlap"):
+        sparse_mla(*call_args(tensors), **call_kwargs(policy), softmax_lse=lse, workspace=workspace)
+    # A debug image that starts in the workspace's last 256 bytes.
+    debug_bytes = policy["T"] * policy["S"] * 8
+    big = torch.empty(workspace.numel() + debug_bytes, dtype=torch.uint8, device=device)
+    debug = big[workspace.numel() - 256 : workspace.numel() - 256 + debug_bytes].view(torch.int32)
+    debug = debug.view(policy["T"], policy["S"], 2)
+    with pytest.raises(ValueError, match="overlap"):
+        sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug, workspace=big[: workspace.numel()])
+    out_alias = tensors["attention_out"].view(torch.uint8).view(-1)[: workspace.numel()]
+    if out_alias.numel() == workspace.numel():
+        with pytest.raises(ValueError, match="overlap"):
+            sparse_mla(*call_args(tensors), **call_kwargs(policy), workspace=out_alias)
+
+
 def metadata_view(inputs):
     """The integer metadata of device-built inputs as an oracle data dict (no rows)."""
     return {k: inputs.host[k] for k in INT_KEYS}

@@ -201,6 +201,24 @@ def test_large_topk_matches_the_oracle(device, topk):
     assert np.array_equal(got, expect)
 
 
+@pytest.mark.parametrize("topk", [4097, 8192])
+def test_topk_beyond_the_wide_buffer_matches_the_oracle(device, topk):
+    """Rows over 32K positions run the 1024-thread form, whose filter buffer
+    holds 4096 entries: a selection of more than that goes straight to the
+    whole-row selection (no filter pass can hold it). Ties and a request whose
+    cutoff leaves fewer candidates than TOPK are included."""
+    rng = np.random.default_rng(topk)
+    c = 40000
+    cu = np.array([0, 5, 9], np.int32)
+    seq_cmp, residual = np.array([c, 6000], np.int32), np.array([1, 0], np.int32)
+    scores = rng.normal(size=(9, c)).astype(np.float32)
+    scores[1, ::7] = 1.5  # a block of equal keys around the threshold
+    scores[2] = np.round(scores[2] * 4) / 4
+    got = run(device, scores, cu, seq_cmp, residual, topk, 2)
+    expect = tr.topk_indices(scores, cu, seq_cmp, residual, topk, 2)
+    assert np.array_equal(got, expect)
+
+
 @pytest.mark.parametrize("c,topk", [(1, 1), (3, 2), (4, 1), (7, 16), (33, 33)])
 def test_tiny_rows_many_empty_requests(device, c, topk):
     """Rows of 1-33 positions (the scalar and the 16-byte load paths), TOPK 1
