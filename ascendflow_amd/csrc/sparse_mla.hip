@@ -105,21 +105,32 @@ __device__ __forceinline__ int request_by_search(const SparseArgs& a, int token)
 
 // query_metadata (gather.py:8-35) and the compressed bound (attention.py:339-341)
 // of a token whose request is `batch`.
-__device__ __forceinline__ Geometry token_geometry(const SparseArgs& a, int token, int batch) {
-  const int lo = batch;
+// The request's inputs of the geometry: cu[b], cu[b + 1], seq_ori[b],
+// seq_cmp[b], residual[b].
+struct RequestInputs {
+  int begin, next, seq_ori, seq_cmp, residual;
+};
+__device__ __forceinline__ RequestInputs request_inputs(const SparseArgs& a, int b) {
+  return RequestInputs{a.cu[b], a.cu[b + 1], a.seq_ori[b], a.seq_cmp[b], a.residual[b]};
+}
+// narrowed = ori_topk_length[token].
+__device__ __forceinline__ Geometry geometry_of(const SparseArgs& a, int token, int batch, const RequestInputs& r,
+                                                int narrowed) {
   Geometry g;
-  g.batch = lo;
-  const int begin = a.cu[lo], count = a.cu[lo + 1] - begin, offset = token - begin;
-  g.right = max(0, a.seq_ori[lo] - count + offset + 1);
+  g.batch = batch;
+  const int begin = r.begin, count = r.next - begin, offset = token - begin;
+  g.right = max(0, r.seq_ori - count + offset + 1);
   int visible = min(a.WINDOW, g.right);
-  const int narrowed = a.ori_topk_length[token];
   if (narrowed > 0) visible = min(visible, narrowed);
   g.visible = visible;
-  const int available = a.seq_cmp[lo];
-  const int end = available * a.RATIO + a.residual[lo];
+  const int available = r.seq_cmp;
+  const int end = available * a.RATIO + r.residual;
   g.cutoff = max(0, end - count + offset + 1) / a.RATIO;
   g.count_cmp = max(0, min(a.TOPK, min(available, g.cutoff)));
   return g;
+}
+__device__ __forceinline__ Geometry token_geometry(const SparseArgs& a, int token, int batch) {
+  return geometry_of(a, token, batch, request_inputs(a, batch), a.ori_topk_length[token]);
 }
 
 // Resolve gather slot s of a token (window slot s < WINDOW, else compressed
@@ -161,11 +172,15 @@ __device__ __forceinline__ const T* row_pointer(const SparseArgs& a, uint32_t en
 // Resolves the selected rows of `token` into row_list (LDS) in slot order
 // (window positions, then compressed ranks) and returns their count. Every
 // one of the NTH threads of the workgroup must call it (workgroup barriers);
-// wave_count is LDS scratch of [GP][NTH / 64], request_scratch of [NTH / 64].
-// Three dependent global round trips: the request count with the compressed
-// indices, then the geometry with the compressed page lookups, then the window
-// page lookups (gather.py:8-60, 116-127; attention.py:339-341); GP passes of
-// NTH slots go together, so WINDOW + TOPK <= GP * NTH takes one such sequence.
+// wave_count is LDS scratch of [GP][NTH / 64], request_scratch of
+// [NTH / 64 + 5]. With B <= NTH, two dependent global round trips: the
+// request count, the compressed indices and every request's geometry inputs
+// (thread b those of request b; the thread of the token's request hands them
+// to the others through LDS), then the compressed and the window page lookups
+// together (gather.py:8-60, 116-127; attention.py:339-341). Larger B loads
+// the geometry inputs once the request is known, and the window lookups wait
+// for them (three round trips). GP passes of NTH slots go together, so
+// WINDOW + TOPK <= GP * NTH takes one such sequence.
 template <int NTH, int GP>
 __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint32_t* row_list,
                                             int (*wave_count)[NTH / 64], int* request_scratch,
@@ -178,6 +193,10 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
   // have cu[b] == cu[b+1] and are skipped).
   int below = 0;
   for (int b = tid; b < a.B; b += NTH) below += a.cu[b] <= token ? 1 : 0;
+  const bool early = a.B <= NTH;  // uniform
+  RequestInputs mine{0, 0, 0, 0, 0};
+  if (early && tid < a.B) mine = request_inputs(a, tid);
+  const int narrowed = a.ori_topk_length[token];
   int index[GP];
   auto load_indices = [&](int s0) {
 #pragma unroll
@@ -197,7 +216,7 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
   const int batch = requests - 1;
 
   // The compressed page lookups need only the request and the indices, so
-  // they go out with the geometry loads; the window lookups need the geometry.
+  // they go out first; the window lookups need the geometry.
   const int cpage = a.PAGE / a.RATIO;
   const int* cmp_row = a.cmp_table + (size_t)batch * a.table_width;
   const int* ori_row = a.ori_table + (size_t)batch * a.table_width;
@@ -208,7 +227,21 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
       cblock[k] = index[k] >= 0 ? cmp_row[min(index[k] / cpage, a.table_width - 1)] : -1;
   };
   load_cmp_blocks();
-  geo = token_geometry(a, token, batch);
+  if (early) {
+    int* inputs = request_scratch + NWV;
+    if (tid == batch) {
+      inputs[0] = mine.begin;
+      inputs[1] = mine.next;
+      inputs[2] = mine.seq_ori;
+      inputs[3] = mine.seq_cmp;
+      inputs[4] = mine.residual;
+    }
+    __syncthreads();
+    geo = geometry_of(a, token, batch, RequestInputs{inputs[0], inputs[1], inputs[2], inputs[3], inputs[4]},
+                      narrowed);
+  } else {
+    geo = geometry_of(a, token, batch, request_inputs(a, batch), narrowed);
+  }
   const int slots = a.WINDOW + geo.count_cmp;
   // Slot s (window slot s < WINDOW, else compressed rank s - WINDOW) resolves
   // to a tagged physical row as in resolve_slot (gather.py:38-60, 116-127).
@@ -282,13 +315,13 @@ template <int NTH>
 __global__ __launch_bounds__(NTH) void sparse_plan_kernel(SparseArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t plan_list[];
   // One wave per token, ten passes of 64 slots: WINDOW + TOPK = 640 in one
-  // round-trip sequence. The kernel is latency-bound (three dependent round
-  // trips per token); one-wave workgroups let every token of a Q8K prefill be
-  // resident at once (four waves per token took ~4 rounds of residency:
-  // prefill 0.7-1.2% slower).
+  // round-trip sequence. The kernel is latency-bound (two or three dependent
+  // round trips per token); one-wave workgroups let every token of a Q8K
+  // prefill be resident at once (four waves per token took ~4 rounds of
+  // residency: prefill 0.7-1.2% slower).
   constexpr int GP = 10;
   __shared__ int wave_count[GP][NTH / 64];
-  __shared__ int request_scratch[NTH / 64];
+  __shared__ int request_scratch[NTH / 64 + 5];
   const int token = blockIdx.x;
   Geometry geo;
   const int n = resolve_rows<NTH, GP>(a, token, plan_list, wave_count, request_scratch, geo);
@@ -401,7 +434,10 @@ constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
 // KV uses a ring of NS tiles (3: one chunk in flight; 4: two, for streams whose
 // rows come from HBM): during step i the score waves read tile i and the output
 // waves tile i-1, so the fetch at the top of step i never overwrites a tile
-// still in use.
+// still in use. With D = 512 and NQ = NP = 4 the output waves issue the whole
+// fetch (8 rows each) and the score waves, whose step is the longer one, only
+// wait at the barrier (decode B64 x 6: 3% faster than every wave fetching 4
+// rows); other shapes spread the fetch over every wave.
 template <int DT, int D, int NQ, int NP, int NS>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
@@ -481,11 +517,11 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       }
     }
   };
-  __shared__ int request_scratch[NW];
+  __shared__ int request_scratch[NW + 5];
   int n_rows;
   {
     // Q does not depend on the row list: its copy goes out first and lands
-    // while the rows are resolved (three dependent round trips).
+    // while the rows are resolved (two or three dependent round trips).
     copy_q();
     Geometry geo;
     n_rows = resolve_rows<NT, 2>(a, token, row_list, wave_count, request_scratch, geo);
@@ -526,30 +562,35 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   // set inside the same asm statement; nothing else in this kernel uses M0.
   // Completion is tracked with vmcnt: when a step waits, the only vector
   // memory loads in flight are the previous fetch's.
-  // With D = 512 one wave load covers exactly one 1 KiB row, so a wave takes
-  // PIECES consecutive rows whose list entries and addresses are wave-uniform
-  // (scalar registers), and the entries are read one step ahead.
+  // With D = 512 one wave load covers exactly one 1 KiB row, so a fetching
+  // wave takes FPW consecutive rows whose list entries and addresses are
+  // wave-uniform (scalar registers), and the entries are read one step ahead.
+  // OWN_FETCH: only the output waves fetch (FPW = CHUNK / NP rows each).
   constexpr bool ROW_LOADS = (UNITS == 64);
+  constexpr bool OWN_FETCH = ROW_LOADS && NQ == 4 && NP == 4;
+  constexpr int FPW = OWN_FETCH ? CHUNK / NP : PIECES;
+  const bool fetcher = !OWN_FETCH || !scorer;
+  const int fw = OWN_FETCH ? wave - NQ : wave;  // this wave's index among the fetching waves
   const char* ori = (const char*)a.ori_kv;
   const char* cmp = (const char*)a.cmp_kv;
   const uint32_t kv_base = lds_address(kv_lds[0]);
   auto tile_address = [&](int chunk) {
     return opaque_uniform(kv_base + (uint32_t)(chunk % NS) * (CHUNK * ROW_BYTES));
   };
-  uint32_t unit_offset[PIECES];  // ROW_LOADS: byte offset of the unit this lane loads
+  uint32_t unit_offset[FPW];  // ROW_LOADS: byte offset of the unit this lane loads
 #pragma unroll
-  for (int p = 0; p < PIECES; ++p) unit_offset[p] = (uint32_t)((lane ^ ((wave * PIECES + p) & 15)) << 4);
-  uint32_t entry_next[PIECES];
+  for (int p = 0; p < FPW; ++p) unit_offset[p] = (uint32_t)((lane ^ ((fw * FPW + p) & 15)) << 4);
+  uint32_t entry_next[FPW];
   auto read_entries = [&](int chunk) {
 #pragma unroll
-    for (int p = 0; p < PIECES; ++p) entry_next[p] = row_list[list_chunk(chunk) * CHUNK + wave * PIECES + p];
+    for (int p = 0; p < FPW; ++p) entry_next[p] = row_list[list_chunk(chunk) * CHUNK + fw * FPW + p];
   };
   auto fetch = [&](int chunk) {
     const uint32_t tile = tile_address(chunk);
     if constexpr (ROW_LOADS) {
 #pragma unroll
-      for (int p = 0; p < PIECES; ++p) {
-        const int r = wave * PIECES + p;
+      for (int p = 0; p < FPW; ++p) {
+        const int r = fw * FPW + p;
         const uint32_t e = __builtin_amdgcn_readfirstlane(entry_next[p]);
         const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES;
         const uint32_t dst = tile + (uint32_t)(r * ROW_BYTES);
@@ -573,18 +614,18 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   // Pipeline step i: wait for KV(i), barrier, fetch KV(i + AHEAD), then the
   // role's work. Loads complete in issue order, so KV(i) has landed once at
   // most the younger batch (KV(i + 1), with a 4-tile ring) is in flight.
-  if (chunks > 0) {
+  if (fetcher && chunks > 0) {
     if constexpr (ROW_LOADS) read_entries(0);
     fetch(0);
     if (AHEAD > 1 && chunks > 1) {
       fetch(1);
       // Q has landed once at most the loads of the two prologue fetches are in flight.
-      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * PIECES) & 15) | (((2 * PIECES) >> 4) << 14));
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * FPW) & 15) | (((2 * FPW) >> 4) << 14));
     } else {
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (FPW & 15) | ((FPW >> 4) << 14));
     }
   } else {
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's Q loads
   }
   block_barrier();
   // Score wave fragments: this lane holds head 16 * wave + i16 (tile row r),
@@ -599,23 +640,23 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
       qf[j] = *lds_at<x8>(q_lds + (uint32_t)(r * ROW_BYTES + (((4 * j + g) ^ (r & 15)) << 4)));
   }
   auto step_begin = [&](int i) {
-    if (i < chunks) {
+    if (fetcher && i < chunks) {
       if (AHEAD > 1 && i + 1 < chunks)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (PIECES & 15) | ((PIECES >> 4) << 14));
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (FPW & 15) | ((FPW >> 4) << 14));
       else
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     block_barrier();
-    if (i + AHEAD < chunks) fetch(i + AHEAD);
+    if (fetcher && i + AHEAD < chunks) fetch(i + AHEAD);
   };
 
   // The swizzle only permutes units within aligned groups of 16 (256 bytes),
   // so a fragment address is a per-lane base plus a compile-time offset.
   if (scorer) {
     // ---- 4a. score wave: QK, online softmax, P -------------------------------
-    // Here the score waves' step (QK, softmax, their share of the fetch) is the
-    // longer one: they get the higher wave priority (the output waves' instead
-    // made decode 6% slower).
+    // Here the score waves' step (QK and softmax, plus their share of the
+    // fetch unless OWN_FETCH) is the longer one: they get the higher wave
+    // priority (the output waves' instead made decode 6% slower).
     __builtin_amdgcn_s_setprio(2);
     // The running max (log2 units) starts at the sink and is raised (with l
     // rescaled here and O rescaled by the output waves) only when a head's max
