@@ -13,7 +13,7 @@
 //      row list of physical row ids. With a workspace and at least two work
 //      items per CU, a plan kernel does this for every token first and a
 //      persistent form (sparse_mla_persistent_kernel) streams the tokens of
-//      each CU through one pipeline, so the three dependent global round trips
+//      each CU through one pipeline, so the dependent global round trips
 //      and the pipeline fill no longer idle the matrix cores at token starts;
 //   2. stream the listed rows through a 3- or 4-stage ring of XOR-swizzled
 //      LDS tiles of CHUNK rows with the load-to-LDS path
