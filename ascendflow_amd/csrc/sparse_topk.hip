@@ -15,10 +15,14 @@
 // each score. sparse_topk_filter (rows up to 256K positions; 256 threads up
 // to 32K positions, 1024 beyond):
 //   1. sample: four keys per thread, in blocks of 16 consecutive positions
-//      evenly spaced over the row; a radix selection on the sample gives an
-//      estimate of the threshold, taken at 1.25x the expected rank plus 8
-//      (256 threads) or twice it plus 16 (1024), so that somewhat more than
-//      `take` keys reach it;
+//      evenly spaced over the row (issued with the request lookup, over the
+//      whole allocated row, and kept when the token's candidates cover at
+//      least half of it; shorter rows are sampled again over their
+//      candidates); a two-digit radix selection on the sample (the top 22
+//      bits of the key: an estimate needs no more) gives an estimate of the
+//      threshold, taken at 1.25x the expected rank plus 8 (256 threads) or
+//      twice it plus 16 (1024), so that somewhat more than `take` keys reach
+//      it;
 //   2. filter: one streaming pass over the row (16-byte loads, several in
 //      flight per thread) appends every key >= estimate, with its position,
 //      to an LDS buffer (wave ballots, one LDS atomic per wave and step);
@@ -82,6 +86,19 @@ struct TokenBounds {
   int cand, take;
 };
 
+// Bounds of a token of the request holding cu[b] = begin, cu[b + 1] = next,
+// seq_cmp[b] = available, residual[b] = residual.
+__device__ __forceinline__ TokenBounds bounds_of(const TopkArgs& a, int token, int begin, int next, int available,
+                                                 int residual) {
+  const int count_q = next - begin, offset = token - begin;
+  const int end = available * a.RATIO + residual;
+  const int cutoff = max(0, end - count_q + offset + 1) / a.RATIO;
+  TokenBounds tb;
+  tb.cand = (int)min<int64_t>(cutoff, a.C);
+  tb.take = min(max(0, min(a.TOPK, min(available, cutoff))), tb.cand);
+  return tb;
+}
+
 __device__ __forceinline__ TokenBounds token_bounds(const TopkArgs& a, int token) {
   int lo = 0, n = a.B;
   while (n > 1) {
@@ -93,14 +110,7 @@ __device__ __forceinline__ TokenBounds token_bounds(const TopkArgs& a, int token
       n = half;
     }
   }
-  const int count_q = a.cu[lo + 1] - a.cu[lo], offset = token - a.cu[lo];
-  const int available = a.seq_cmp[lo];
-  const int end = available * a.RATIO + a.residual[lo];
-  const int cutoff = max(0, end - count_q + offset + 1) / a.RATIO;
-  TokenBounds tb;
-  tb.cand = (int)min<int64_t>(cutoff, a.C);
-  tb.take = min(max(0, min(a.TOPK, min(available, cutoff))), tb.cand);
-  return tb;
+  return bounds_of(a, token, a.cu[lo], a.cu[lo + 1], a.seq_cmp[lo], a.residual[lo]);
 }
 
 // Writes the -1 tail and the trivial selections; true when nothing is left.
@@ -182,19 +192,22 @@ struct RadixLds {
 // Radix selection of the rank-th largest key among those a key source
 // yields: for_each_key(f) calls f(key) for every key of the source held by
 // this thread. Returns that key, with *need_out = how many keys equal to it
-// are among the rank largest. Per digit: LDS histogram atomics, one barrier,
-// wave 0 finds the digit's bin (a scan over lanes from the top bin) while the
-// other waves clear the other histogram, one barrier. Expects
-// hist[parity] cleared and leaves hist[parity] (flipped) cleared.
-template <int THREADS, bool PACKED, typename ForEachKey>
+// are among the rank largest; with PASSES < 3 digits, the key's leading
+// DIGIT_SHIFT[PASSES - 1] bits (the rest zero) and the count for that prefix.
+// Per digit: LDS histogram atomics, one barrier, wave 0 finds the digit's bin
+// (a scan over lanes from the top bin) while the other waves clear the other
+// histogram, one barrier. Expects hist[parity] cleared and leaves
+// hist[parity] (flipped) cleared.
+template <int THREADS, bool PACKED, int PASSES = 3, typename ForEachKey>
 __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int rank, RadixLds<PACKED>& lds, int& parity,
                                                  int* need_out) {
+  static_assert(PASSES >= 1 && PASSES <= 3, "one to three digits");
   static_assert(THREADS > 64, "the histogram is cleared by the waves other than wave 0");
   const int tid = threadIdx.x, lane = tid & 63;
   uint32_t prefix = 0, prefix_mask = 0;
   int need = rank;
 #pragma unroll
-  for (int pass = 0; pass < 3; ++pass) {
+  for (int pass = 0; pass < PASSES; ++pass) {
     const int shift = DIGIT_SHIFT[pass], bins = 1 << DIGIT_WIDTH[pass];
     const int cur = parity;
     for_each_key([&](uint32_t k) {
@@ -344,8 +357,63 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
   __shared__ RadixLds<COMPACT> radix;
   __shared__ int scan_scratch[2 * THREADS / 64];
   __shared__ int reached;
-  const int token = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-  const TokenBounds tb = token_bounds(a, token);
+  __shared__ int request_lds[4];
+  constexpr int WAVES = THREADS / 64;
+  const int token = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // 1. Sample: S keys in blocks of 16 consecutive positions (64 bytes), the
+  // S / 16 blocks evenly spaced over a range of n positions (block b from
+  // position floor(b n / (S / 16))), so the sample touches few cache lines;
+  // thread t holds samples 4t .. 4t + 3. The first sample, S = min(TK_SAMPLES
+  // THREADS, C) over the whole allocated row (n = C), goes out before the
+  // request lookup; its keys at positions past the token's candidates are
+  // left out, and when the candidates cover less than half of the row (or C
+  // < TK_SAMPLES THREADS) the row is sampled again over them (n = cand,
+  // S = min(TK_SAMPLES THREADS, cand), a row shorter than that whole).
+  const int samples_c = (int)min<int64_t>(TK_SAMPLES * THREADS, a.C);
+  const int blocks_c = samples_c / 16;
+  const __amdgpu_buffer_rsrc_t rsrc_row = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.scores + (size_t)token * a.C), (short)0, (int)(a.C * 4), BUFFER_WORD3);
+  uint32_t sample[TK_SAMPLES];
+  int sample_pos[TK_SAMPLES];
+#pragma unroll
+  for (int j = 0; j < TK_SAMPLES; ++j) {
+    const int i = tid * TK_SAMPLES + j;
+    sample_pos[j] = samples_c < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * a.C) / blocks_c) + (i & 15);
+    sample[j] =
+        i < samples_c ? score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_row, sample_pos[j] * 4, 0, 0)))
+                      : 0u;
+  }
+  // Request lookup. B <= THREADS: one round trip, thread b loading request
+  // b's cu[b], cu[b + 1], seq_cmp[b] and residual[b]; the token's request is
+  // #{b: cu[b] <= token} - 1 (as in token_bounds), whose thread hands its
+  // values to the others through LDS. Larger B: the binary search.
+  TokenBounds tb;
+  if (a.B <= THREADS) {
+    int begin = 0, next = 0, available = 0, residual = 0;
+    if (tid < a.B) {
+      begin = a.cu[tid];
+      next = a.cu[tid + 1];
+      available = a.seq_cmp[tid];
+      residual = a.residual[tid];
+    }
+    const int below = __popcll(__ballot(tid < a.B && begin <= token));
+    if (lane == 0) scan_scratch[wave] = below;
+    __syncthreads();
+    int requests = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) requests += scan_scratch[w];
+    if (tid == requests - 1) {
+      request_lds[0] = begin;
+      request_lds[1] = next;
+      request_lds[2] = available;
+      request_lds[3] = residual;
+    }
+    __syncthreads();
+    tb = bounds_of(a, token, request_lds[0], request_lds[1], request_lds[2], request_lds[3]);
+  } else {
+    tb = token_bounds(a, token);
+  }
   int32_t* out = a.indices + (size_t)token * a.TOPK;
   if (trivial_selection<THREADS>(a, tb, out)) return;
   const int cand = tb.cand, take = tb.take, words = (cand + 31) >> 5;
@@ -353,25 +421,39 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
   uint32_t* equal_bits = bitmaps + words;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(a.scores + (size_t)token * a.C), (short)0, cand * 4, BUFFER_WORD3);
-
-  // 1. Sample: S = min(TK_SAMPLES THREADS, cand) keys in blocks of 16
-  // consecutive positions (64 bytes), the S / 16 blocks evenly spaced over
-  // the row (block b from position floor(b cand / (S / 16))), so the sample
-  // touches few cache lines; a row shorter than TK_SAMPLES THREADS is
-  // sampled whole. Thread t holds samples 4t .. 4t + 3.
-  const int samples = min(TK_SAMPLES * THREADS, cand);
-  const int blocks = samples / 16;
-  uint32_t sample[TK_SAMPLES];
+  const bool whole_row_sample = samples_c == TK_SAMPLES * THREADS && 2 * (int64_t)cand >= a.C;  // uniform
+  int samples = 0;           // keys in the sample
+  uint32_t sample_mask = 0;  // bit j: sample[j] is one of them
+  if (whole_row_sample) {
+    int mine = 0;
 #pragma unroll
-  for (int j = 0; j < TK_SAMPLES; ++j) {
-    const int i = tid * TK_SAMPLES + j;
-    const int p = samples < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * cand) / blocks) + (i & 15);
-    sample[j] = i < samples ? score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, p * 4, 0, 0))) : 0u;
+    for (int j = 0; j < TK_SAMPLES; ++j) {
+      const bool in_row = sample_pos[j] < cand;
+      sample_mask |= in_row ? 1u << j : 0u;
+      mine += in_row ? 1 : 0;
+    }
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) mine += __shfl_xor(mine, d);
+    if (lane == 0) scan_scratch[WAVES + wave] = mine;  // summed after the barrier below
+  } else {
+    samples = min(TK_SAMPLES * THREADS, cand);
+    const int blocks = samples / 16;
+#pragma unroll
+    for (int j = 0; j < TK_SAMPLES; ++j) {
+      const int i = tid * TK_SAMPLES + j;
+      const int p = samples < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * cand) / blocks) + (i & 15);
+      sample[j] = i < samples ? score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, p * 4, 0, 0))) : 0u;
+      sample_mask |= i < samples ? 1u << j : 0u;
+    }
   }
   for (int i = tid; i < 2 * words; i += THREADS) bitmaps[i] = 0u;
   for (int i = tid; i < RadixLds<COMPACT>::WORDS; i += THREADS) radix.hist[0][i] = 0u;
   if (tid == 0) reached = 0;
   __syncthreads();
+  if (whole_row_sample) {
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) samples += scan_scratch[WAVES + w];
+  }
   int parity = 0, unused = 0;
 
   // 2. Filter: keys >= estimate (>= 1, so never a position past the row),
@@ -391,11 +473,11 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
   // buffer's capacity no pass can, so the row goes straight to the whole-row
   // selection below instead of being streamed by every filter round first.
   for (int round = 0; take <= CAP && round < TK_FILTER_ROUNDS; ++round) {
-    const uint32_t estimate = radix_select<THREADS>(
+    const uint32_t estimate = radix_select<THREADS, COMPACT, 2>(
         [&](auto f) {
 #pragma unroll
           for (int j = 0; j < TK_SAMPLES; ++j)
-            if (tid * TK_SAMPLES + j < samples) f(sample[j]);
+            if ((sample_mask >> j) & 1u) f(sample[j]);
         },
         rank, radix, parity, &unused);  // ends with a barrier: every read of `reached` is done
     if (tid == 0) reached = 0;
