@@ -132,7 +132,10 @@ def release_bindings():
 
 
 def binding_key(device_index, stream, sizes):
-    return (device_index, stream) + sizes
+    # The loaded library is part of the key: a binding's workspace size comes
+    # from that library's workspace query (its split choice), so a binding
+    # made through one library is never handed to another.
+    return (id(_native.library()), device_index, stream) + sizes
 
 
 def _binding(device, stream, sizes, policy, dtype, parts, ring):

@@ -44,6 +44,22 @@ def test_binding_key_separates_sizes_dtype_and_stream():
     assert len(keys) == 6
 
 
+def test_binding_key_separates_libraries():
+    """A binding (and its workspace, sized by the library's own workspace
+    query) belongs to the library that made it: with another library loaded
+    in its place the same call gets a new binding."""
+    from ascendflow_amd import _native
+    base = make()
+    saved = _native._lib
+    try:
+        _native._lib = _native.library(_native.LIB_PATH)  # a second handle of the library
+        assert A.binding_key(0, 7, sizes()) != (id(saved), 0, 7) + sizes()
+        assert make() is not base
+    finally:
+        _native._lib = saved
+    assert make() is base
+
+
 def test_binding_holds_the_calls_parameters_and_workspace_size():
     b = make(T=1024)
     assert (b.params.T, b.params.B, b.params.TOPK, b.params.dtype) == (1024, 4, 512, 0)
