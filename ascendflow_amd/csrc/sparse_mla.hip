@@ -213,7 +213,9 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
   int requests = 0;
 #pragma unroll
   for (int w = 0; w < NWV; ++w) requests += request_scratch[w];
-  const int batch = requests - 1;
+  // At least request 0: cu_seqlens_q starts at 0 <= token, and an input that
+  // breaks that still reads request 0's tables, never memory before them.
+  const int batch = max(requests - 1, 0);
 
   // The compressed page lookups need only the request and the indices, so
   // they go out first; the window lookups need the geometry.

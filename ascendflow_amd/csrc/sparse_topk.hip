@@ -403,7 +403,7 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
     int requests = 0;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) requests += scan_scratch[w];
-    if (tid == requests - 1) {
+    if (tid == max(requests - 1, 0)) {  // request 0 at least (cu[0] = 0 <= token)
       request_lds[0] = begin;
       request_lds[1] = next;
       request_lds[2] = available;
