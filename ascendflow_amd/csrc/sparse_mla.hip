@@ -438,7 +438,7 @@ constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
 // waves tile i-1, so the fetch at the top of step i never overwrites a tile
 // still in use. With D = 512 and NQ = NP = 4 the output waves issue the whole
 // fetch (8 rows each) and the score waves, whose step is the longer one, only
-// wait at the barrier (decode B64 x 6: 3% faster than every wave fetching 4
+// wait at the barrier (decode B64 x 6 ~2% faster than every wave fetching 4
 // rows); other shapes spread the fetch over every wave.
 template <int DT, int D, int NQ, int NP, int NS>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a) {
