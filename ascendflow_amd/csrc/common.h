@@ -76,6 +76,21 @@ __device__ __forceinline__ float sum_over_lane_groups(float v) {
   return a + b;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (every lane active), in
+// DPP moves rather than LDS permutes: shifts by 1, 2, 4 and 8 within each row
+// of 16 lanes (lanes shifted in from outside the row add 0), then row 0's
+// total is added to row 1 and row 2's to row 3 (row_bcast:15 into rows 1, 3),
+// then the total of rows 0-1 to rows 2 and 3 (row_bcast:31 into rows 2, 3).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
 // gfx950 LDS serves 64 four-byte banks (256 bytes) per cycle. Measured lane
 // grouping: a 16-byte read (ds_read_b128) serves, within each 32-lane half, the
 // 16 lanes whose quad index (lane >> 2) & 7 has even parity, then the odd ones;

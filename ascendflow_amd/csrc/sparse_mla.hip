@@ -206,8 +206,7 @@ __device__ __forceinline__ int resolve_rows(const SparseArgs& a, int token, uint
     }
   };
   load_indices(0);
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) below += __shfl_xor(below, d);
+  below = __builtin_amdgcn_readlane(wave_inclusive_scan(below), 63);  // the wave's sum
   if (lane == 0) request_scratch[wave] = below;
   __syncthreads();
   int requests = 0;

@@ -125,16 +125,6 @@ __device__ __forceinline__ bool trivial_selection(const TopkArgs& a, TokenBounds
   return false;
 }
 
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int up = __shfl_up(v, d);
-    if (lane >= d) v += up;
-  }
-  return v;
-}
-
 // Exclusive prefix sums of two values over the workgroup, sharing barriers;
 // totals in total[0..1]. scratch: 2 THREADS / 64 ints of LDS.
 template <int THREADS>
@@ -219,7 +209,7 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
       if (active == 0) return;  // uniform
       const int bin = (int)((k >> shift) & (uint32_t)(bins - 1));
       const int leader = (int)__builtin_ctzll(active);
-      const int lead_bin = __shfl(bin, leader);
+      const int lead_bin = __builtin_amdgcn_readlane(bin, leader);  // leader is wave-uniform
       const uint64_t same = __ballot(counts && bin == lead_bin);
       if (lane == leader) lds.add(cur, lead_bin, __popcll(same));
       else if (counts && bin != lead_bin) lds.add(cur, bin, 1);
@@ -236,7 +226,7 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
       for (int q = 0; q < per; ++q) local += lds.get(cur, bins - 1 - (lane * per + ((q + lane) & (per - 1))));
       const int incl = wave_inclusive_scan(local);
       const int owner = (int)__builtin_ctzll(__ballot(incl - local < need && incl >= need));
-      const int above = __shfl(incl - local, owner);
+      const int above = __builtin_amdgcn_readlane(incl - local, owner);  // owner is wave-uniform
       const int count = lane < per ? lds.get(cur, bins - 1 - (owner * per + lane)) : 0;
       const int incl2 = wave_inclusive_scan(count);
       const int q = (int)__builtin_ctzll(__ballot(lane < per && above + incl2 >= need));
@@ -370,19 +360,27 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
   // left out, and when the candidates cover less than half of the row (or C
   // < TK_SAMPLES THREADS) the row is sampled again over them (n = cand,
   // S = min(TK_SAMPLES THREADS, cand), a row shorter than that whole).
+  // A sample shorter than TK_SAMPLES THREADS is the whole range (block
+  // positions i); otherwise it has SAMPLE_BLOCKS blocks, a power of two, so
+  // floor(b n / SAMPLE_BLOCKS) is a shift. The loads are unconditional
+  // (positions past the buffer's range read 0) and their words are turned
+  // into keys only where they are used, so that the four go out together
+  // with the request lookup's and share its round trip.
+  constexpr int SAMPLE_BLOCKS = TK_SAMPLES * THREADS / 16;
+  constexpr int SAMPLE_SHIFT = __builtin_ctz(SAMPLE_BLOCKS);
+  static_assert((SAMPLE_BLOCKS & (SAMPLE_BLOCKS - 1)) == 0, "sample blocks must be a power of two");
+  auto sample_position = [&](int i, int64_t n, int s) {
+    return s < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * n) >> SAMPLE_SHIFT) + (i & 15);
+  };
   const int samples_c = (int)min<int64_t>(TK_SAMPLES * THREADS, a.C);
-  const int blocks_c = samples_c / 16;
   const __amdgpu_buffer_rsrc_t rsrc_row = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(a.scores + (size_t)token * a.C), (short)0, (int)(a.C * 4), BUFFER_WORD3);
-  uint32_t sample[TK_SAMPLES];
+  uint32_t sample[TK_SAMPLES];  // the score words, then their keys
   int sample_pos[TK_SAMPLES];
 #pragma unroll
   for (int j = 0; j < TK_SAMPLES; ++j) {
-    const int i = tid * TK_SAMPLES + j;
-    sample_pos[j] = samples_c < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * a.C) / blocks_c) + (i & 15);
-    sample[j] =
-        i < samples_c ? score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc_row, sample_pos[j] * 4, 0, 0)))
-                      : 0u;
+    sample_pos[j] = sample_position(tid * TK_SAMPLES + j, a.C, samples_c);
+    sample[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc_row, sample_pos[j] * 4, 0, 0);
   }
   // Request lookup. B <= THREADS: one round trip, thread b loading request
   // b's cu[b], cu[b + 1], seq_cmp[b] and residual[b]; the token's request is
@@ -428,21 +426,22 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
     int mine = 0;
 #pragma unroll
     for (int j = 0; j < TK_SAMPLES; ++j) {
+      sample[j] = score_key(__uint_as_float(sample[j]));  // every sample is in [0, C) here
       const bool in_row = sample_pos[j] < cand;
       sample_mask |= in_row ? 1u << j : 0u;
       mine += in_row ? 1 : 0;
     }
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) mine += __shfl_xor(mine, d);
+    mine = __builtin_amdgcn_readlane(wave_inclusive_scan(mine), 63);
     if (lane == 0) scan_scratch[WAVES + wave] = mine;  // summed after the barrier below
   } else {
     samples = min(TK_SAMPLES * THREADS, cand);
-    const int blocks = samples / 16;
+#pragma unroll
+    for (int j = 0; j < TK_SAMPLES; ++j)
+      sample[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, sample_position(tid * TK_SAMPLES + j, cand, samples) * 4, 0, 0);
 #pragma unroll
     for (int j = 0; j < TK_SAMPLES; ++j) {
       const int i = tid * TK_SAMPLES + j;
-      const int p = samples < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * cand) / blocks) + (i & 15);
-      sample[j] = i < samples ? score_key(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, p * 4, 0, 0))) : 0u;
+      sample[j] = i < samples ? score_key(__uint_as_float(sample[j])) : 0u;
       sample_mask |= i < samples ? 1u << j : 0u;
     }
   }
