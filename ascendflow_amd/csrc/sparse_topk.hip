@@ -163,7 +163,7 @@ constexpr int DIGIT_WIDTH[3] = {11, 11, 10};
 template <bool PACKED>
 struct RadixLds {
   static constexpr int WORDS = PACKED ? TK_BINS / 2 : TK_BINS;
-  uint32_t hist[2][WORDS];
+  alignas(16) uint32_t hist[2][WORDS];
   int choice[2];  // bin of the digit, keys in the bins above it
   __device__ __forceinline__ void add(int parity, int bin, int n) {
     if constexpr (PACKED)
@@ -216,14 +216,27 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
     });
     __syncthreads();
     if (tid < 64) {
-      // Lane l sums bins [bins - (l + 1) per, bins - l per), starting at a
-      // lane-dependent rotation so that the lanes read distinct LDS banks;
-      // the lane whose bins hold the need-th key is found by a scan over the
-      // lanes, then its bins are read one per lane and scanned the same way.
+      // Lane l sums bins [bins - (l + 1) per, bins - l per): U = 2, 4 or 8
+      // aligned 16-byte units of whole words, read in the order c, c + 1, ...
+      // (mod U) with c chosen so that the 16 lanes one ds_read_b128 pass
+      // serves (four quads whose (lane >> 3) & 3 differ) touch 16 distinct
+      // bank groups. Packed words are summed whole: no half-word sum reaches
+      // 2^16. The lane whose bins hold the need-th key is found by a scan over
+      // the lanes, then its bins are read one per lane and scanned the same way.
       const int per = bins / 64;
-      int local = 0;
-#pragma unroll 8  // a full unroll keeps 32 loads in flight and sets the kernel's register peak
-      for (int q = 0; q < per; ++q) local += lds.get(cur, bins - 1 - (lane * per + ((q + lane) & (per - 1))));
+      const int W = PACKED ? per / 2 : per, U = W / 4;
+      const int quad = (lane >> 3) & 3;
+      const int c = U == 2 ? (quad & 1) : U == 4 ? quad : (((lane >> 1) & 1) | (quad << 1));
+      const uint32_t* words = lds.hist[cur] + (bins - (lane + 1) * per) / (PACKED ? 2 : 1);
+      uint32_t sum = 0;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        if (it < U) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(words + 4 * ((c + it) & (U - 1)));
+          sum += (v[0] + v[1]) + (v[2] + v[3]);
+        }
+      }
+      const int local = PACKED ? (int)((sum & 0xffffu) + (sum >> 16)) : (int)sum;
       const int incl = wave_inclusive_scan(local);
       const int owner = (int)__builtin_ctzll(__ballot(incl - local < need && incl >= need));
       const int above = __builtin_amdgcn_readlane(incl - local, owner);  // owner is wave-uniform
@@ -236,7 +249,8 @@ __device__ __forceinline__ uint32_t radix_select(ForEachKey for_each_key, int ra
       }
     } else {
       uint32_t* spare = lds.hist[parity ^ 1];
-      for (int i = tid - 64; i < RadixLds<PACKED>::WORDS; i += THREADS - 64) spare[i] = 0u;
+      for (int i = 4 * (tid - 64); i < RadixLds<PACKED>::WORDS; i += 4 * (THREADS - 64))
+        *reinterpret_cast<u32x4*>(spare + i) = u32x4{0u, 0u, 0u, 0u};
     }
     __syncthreads();
     need -= lds.choice[1];
