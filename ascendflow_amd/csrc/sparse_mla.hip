@@ -385,7 +385,10 @@ constexpr float TAU = 8.0f;
 // feature units of a KV ring tile (STAGE_ROW = the tile's row bytes, unit_base
 // = the wave's first feature unit, SWZ = 15: the tile's own swizzle). The
 // stage is only touched by this wave, whose LDS operations complete in order.
-template <int DT, int DPV, int STAGE_ROW = DPV * 2, int SWZ = DPV / 8 - 1>
+// NT: non-temporal global stores (the write-once O leaves the L2 to the KV
+// rows that other work items of the request read; decode 63.4 -> 61.8 µs,
+// while the persistent prefill kernel measured ~1% slower with them).
+template <int DT, int DPV, int STAGE_ROW = DPV * 2, int SWZ = DPV / 8 - 1, bool NT = false>
 __device__ __forceinline__ void store_head_tile(uint32_t stage, uint32_t unit_base, const f32x4 (&o)[DPV / 16],
                                                 float inv, typename B16<DT>::scalar* out, size_t head_stride,
                                                 int lane) {
@@ -410,7 +413,11 @@ __device__ __forceinline__ void store_head_tile(uint32_t stage, uint32_t unit_ba
     const int h = r * HPI + lane / UR, u = lane % UR;
     const uint32_t unit = (unit_base + (uint32_t)u) ^ (uint32_t)(h & SWZ);
     const u32x4 w = *(const AFA_LDS u32x4*)(uintptr_t)(stage + (uint32_t)(h * STAGE_ROW) + (unit << 4));
-    *(u32x4*)((char*)(out + (size_t)h * head_stride) + u * 16) = w;
+    u32x4* dst = (u32x4*)((char*)(out + (size_t)h * head_stride) + u * 16);
+    if constexpr (NT)
+      __builtin_nontemporal_store(w, dst);
+    else
+      *dst = w;
   }
 }
 
@@ -500,7 +507,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
   // swizzle; each score wave then reads its B-operand fragments (S^T = KV *
   // Q^T) from there once. Loading the fragments straight into registers
   // touches 64-byte pieces of 16 rows per wave load and stalls the issue of
-  // every other load of the workgroup for thousands of cycles.
+  // every other load of the workgroup for thousands of cycles. Q is read once:
+  // the loads are non-temporal, like the O stores.
   const uint32_t q_lds = lds_address(kv_lds[NS - 2]);
   constexpr int Q_LOADS = BMH * ROW_BYTES / 1024;  // 1 KiB wave loads of the Q tile
   static_assert(BMH * ROW_BYTES <= 2 * CHUNK * ROW_BYTES, "Q tile must fit ring tiles 1 and 2");
@@ -513,7 +521,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
         const int pos = k * 64 + lane;  // 16-byte unit position in the tile
         const int r = pos / UNITS, u = pos % UNITS;
         const uint32_t off = (uint32_t)(r * ROW_BYTES + ((u ^ (r & 15)) << 4));
-        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
                          :: "s"(q_lds + (uint32_t)k * 1024u), "v"(off), "s"(q_src) : "memory");
       }
     }
@@ -829,7 +837,8 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
     scalar* out0 = (scalar*)a.out + ((size_t)token * a.H + head0) * D + dbase;
 #pragma unroll
     for (int ht = 0; ht < NQ; ++ht)
-      store_head_tile<DT, DPV>(stage, 0u, o[ht], linv_lds[16 * ht + i16], out0 + (size_t)16 * ht * D, D, lane);
+      store_head_tile<DT, DPV, DPV * 2, DPV / 8 - 1, true>(stage, 0u, o[ht], linv_lds[16 * ht + i16],
+                                                           out0 + (size_t)16 * ht * D, D, lane);
   }
 }
 
