@@ -79,6 +79,7 @@ struct SparseArgs {
   int32_t parts;         // parts each split (token, head tile) key is divided into (one-item kernel)
   int32_t split_from;    // first split (token, head tile) key; keys below it run whole
   int32_t ring;          // KV ring tiles of the persistent kernel (3 or 4)
+  int32_t stream_kv;     // one-item kernel: non-temporal KV row loads (few query tokens per request)
   float scale;
 };
 
@@ -446,7 +447,7 @@ constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
 // fetch (8 rows each) and the score waves, whose step is the longer one, only
 // wait at the barrier (decode B64 x 6 ~2% faster than every wave fetching 4
 // rows); other shapes spread the fetch over every wave.
-template <int DT, int D, int NQ, int NP, int NS>
+template <int DT, int D, int NQ, int NP, int NS, bool STREAM_KV = false>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
@@ -603,8 +604,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
         const uint32_t e = __builtin_amdgcn_readfirstlane(entry_next[p]);
         const char* row = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES;
         const uint32_t dst = tile + (uint32_t)(r * ROW_BYTES);
-        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-                         :: "s"(dst), "v"(unit_offset[p]), "s"(row) : "memory");
+        if constexpr (STREAM_KV)
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+                           :: "s"(dst), "v"(unit_offset[p]), "s"(row) : "memory");
+        else
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                           :: "s"(dst), "v"(unit_offset[p]), "s"(row) : "memory");
       }
       if (chunk + 1 < chunks) read_entries(chunk + 1);
     } else {
@@ -615,8 +620,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a
         const uint32_t e = row_list[list_chunk(chunk) * CHUNK + r];
         const char* src = ((e & CMP_BIT) ? cmp : ori) + (size_t)(e & ~CMP_BIT) * ROW_BYTES + ((upos ^ (r & 15)) << 4);
         const uint32_t dst = tile + (uint32_t)((wave * 64 + p * NT) * 16);
-        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                         :: "s"(dst), "v"(src) : "memory");
+        if constexpr (STREAM_KV)
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt"
+                           :: "s"(dst), "v"(src) : "memory");
+        else
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                           :: "s"(dst), "v"(src) : "memory");
       }
     }
   };
@@ -1614,6 +1623,13 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   a.parts = split.parts;
   a.split_from = (int32_t)split.split_from;
   a.ring = p->ring != 0 ? p->ring : (kv_cache_bytes(p) > INFINITY_CACHE_BYTES ? 4 : 3);
+  // Non-temporal KV row loads in the one-item kernel when requests have at
+  // most 16 query tokens on average (decode and multi-token decode: B64 x 6
+  // 62.7 -> 59.8 µs, 85 keys 72.4 -> 69.3 µs). Many tokens of one request
+  // share its rows through the L2, which these loads give up: one request of
+  // 500 tokens measured 58.0 -> 63.4 µs with them (and the persistent prefill
+  // kernel 43% slower).
+  a.stream_kv = (int64_t)p->T <= 16 * (int64_t)p->B ? 1 : 0;
   a.scale = p->scale;
   return a;
 }
@@ -1690,6 +1706,17 @@ static int launch_persistent(const SparseArgs& a, int ring, hipStream_t stream) 
   return (int)hipGetLastError();
 }
 
+// After the one-item kernel: the merge of split keys, if any.
+template <int DT, int D, int NQ, int NP>
+static int after_one_item(const SparseArgs& a, int64_t tiles, hipStream_t stream) {
+  if (a.parts < 2) return (int)hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((sparse_merge_kernel<DT, D, NQ, NP>), dim3((unsigned)((tiles - a.split_from) * NP * NQ)),
+                     dim3(merge_threads<D, NP>()), 0, stream, a);
+  return (int)hipGetLastError();
+}
+
 template <int DT, int D, int NQ, int NP>
 static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.list_pad * sizeof(uint32_t);
@@ -1715,20 +1742,33 @@ static int launch_fused(const SparseArgs& a, hipStream_t stream) {
   // short streams whose rows mostly come from HBM; then the merge of split keys.
   const int64_t items = a.split_from + (tiles - a.split_from) * a.parts;
   const unsigned blocks = (unsigned)items;
+  // The non-temporal KV form (a.stream_kv) exists for D = 512, the decode
+  // shape; a uniform branch in the fetch instead of a second kernel cost
+  // 8-11% on every call of the first.
   if (fits_lds<sparse_mla_kernel<DT, D, NQ, NP, 4>>(lds) == AFA_OK) {
+    if constexpr (D == 512) {
+      if (a.stream_kv) {
+        hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 4, true>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream,
+                           a);
+        return after_one_item<DT, D, NQ, NP>(a, tiles, stream);
+      }
+    }
     hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 4>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   } else {
     const int fit = fits_lds<sparse_mla_kernel<DT, D, NQ, NP, 3>>(lds);
     if (fit) return fit;
+    if constexpr (D == 512) {
+      if (a.stream_kv) {
+        hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 3, true>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream,
+                           a);
+        return after_one_item<DT, D, NQ, NP>(a, tiles, stream);
+      }
+    }
     hipLaunchKernelGGL((sparse_mla_kernel<DT, D, NQ, NP, 3>), dim3(blocks), dim3((NQ + NP) * 64), lds, stream, a);
   }
-  if (a.parts < 2) return (int)hipGetLastError();
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((sparse_merge_kernel<DT, D, NQ, NP>), dim3((unsigned)((tiles - a.split_from) * NP * NQ)),
-                     dim3(merge_threads<D, NP>()), 0, stream, a);
-  return (int)hipGetLastError();
+  return after_one_item<DT, D, NQ, NP>(a, tiles, stream);
 }
+
 
 // BM = 16 * NQ heads per workgroup: 4 score + 4 output waves for BM = 64,
 // 2 + 2 for BM = 32.
