@@ -414,6 +414,27 @@ def test_decode_b64x6_ctx128k_all_tokens(device):
 
 
 
+@pytest.mark.parametrize("per_request", [16, 17])
+def test_decode_either_side_of_the_streaming_kv_threshold(device, per_request):
+    """The one-item kernel loads KV rows non-temporally for calls of at most 16
+    query tokens per request (T <= 16 B) and with ordinary loads above: both
+    instantiations (D = 512) match the oracle on every token, with the keys
+    split automatically (these calls fill less than one round of CUs) and
+    whole."""
+    from ascendflow_amd.sparse_attention import sparse_mla
+    from ascendflow_amd.sparse_attention.inputs import make_inputs, measurement_policy
+
+    print(f"\n[sparse] B2 x {per_request} ctx 8192", flush=True)
+    policy = measurement_policy(batch=2, query_tokens=per_request, context=8192)
+    inputs = make_inputs(policy, 8192, device=device)
+    tokens = list(range(policy["T"]))
+    check_measured(inputs, tokens, device, split=True)
+    sparse_mla(*inputs.call_args(), **inputs.call_kwargs(), parts=1)
+    torch.cuda.synchronize()
+    assert_close(inputs.tensors["attention_out"].float().cpu().numpy(),
+                 sr.oracle_fp32(host_view(inputs, tokens), policy, tokens), policy["DTYPE"])
+
+
 @pytest.mark.parametrize("batch", [1, 4, 48])
 def test_decode_small_batches_split_automatically(device, batch):
     """Decode with few requests (x 6 queries at 128K): the library splits the
