@@ -79,7 +79,7 @@ struct SparseArgs {
   int32_t parts;         // parts each split (token, head tile) key is divided into (one-item kernel)
   int32_t split_from;    // first split (token, head tile) key; keys below it run whole
   int32_t ring;          // KV ring tiles of the persistent kernel (3 or 4)
-  int32_t stream_kv;     // one-item kernel: non-temporal KV row loads (few query tokens per request)
+  int32_t stream_kv;     // few query tokens per request: non-temporal KV, Q and O accesses (D = 512)
   float scale;
 };
 
@@ -877,7 +877,7 @@ struct Cursor {
 //    sink's e^(sink - m)), its output accumulators are cleared on its first PV
 //    step, and its denominator travels through LDS slot item & 1.
 // The first item's Q goes through LDS as in sparse_mla_kernel.
-template <int DT, int D, int NQ, int NP, int NS, bool CLAMP>
+template <int DT, int D, int NQ, int NP, int NS, bool CLAMP, bool STREAM = false>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
   typedef typename B16<DT>::x8 x8;
@@ -1018,8 +1018,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
         const int r = ow * PIECES + p;
         const uint32_t e = __builtin_amdgcn_readfirstlane(entry_next[p]);
         const char* row = row_of(e);
-        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-                         :: "s"(tile + (uint32_t)(r * ROW_BYTES)), "v"(unit_offset[p]), "s"(row) : "memory");
+        if constexpr (STREAM)
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+                           :: "s"(tile + (uint32_t)(r * ROW_BYTES)), "v"(unit_offset[p]), "s"(row) : "memory");
+        else
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                           :: "s"(tile + (uint32_t)(r * ROW_BYTES)), "v"(unit_offset[p]), "s"(row) : "memory");
       }
     } else {
       const AFA_LDS uint32_t* l = lds_at<uint32_t>(list_address(k.j));
@@ -1030,8 +1034,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
         const int r = flat / UNITS, upos = flat % UNITS;
         const uint32_t e = l[k.list_chunk() * CHUNK + r];
         const char* src = row_of(e) + ((upos ^ (r & 15)) << 4);
-        __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                         :: "s"(tile + (uint32_t)((ow * 64 + p * NO) * 16)), "v"(src) : "memory");
+        if constexpr (STREAM)
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt"
+                           :: "s"(tile + (uint32_t)((ow * 64 + p * NO) * 16)), "v"(src) : "memory");
+        else
+          __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                           :: "s"(tile + (uint32_t)((ow * 64 + p * NO) * 16)), "v"(src) : "memory");
       }
     }
   };
@@ -1100,7 +1108,12 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
           const int head = item_head0(cur.j + 1) + 16 * wave + i16;
           const scalar* q_row = (const scalar*)a.q + ((size_t)item_token(cur.j + 1) * a.H + head) * D + 8 * g;
 #pragma unroll
-          for (int k = 0; k < QK_STEPS; ++k) qf_next[k] = *(const x8*)(q_row + 32 * k);
+          for (int k = 0; k < QK_STEPS; ++k) {
+            if constexpr (STREAM)
+              qf_next[k] = __builtin_nontemporal_load((const x8*)(q_row + 32 * k));
+            else
+              qf_next[k] = *(const x8*)(q_row + 32 * k);
+          }
           // Used (scaled) only when the next item starts: vector loads retire
           // in order, so consuming it here would wait for all of Q's loads,
           // a full HBM round trip at every item start.
@@ -1218,7 +1231,7 @@ __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(S
 #pragma unroll
       for (int ht = 0; ht < NQ; ++ht) {
         const float inv = 1.0f / l_lds[par][16 * ht + i16];
-        store_head_tile<DT, DPV, ROW_BYTES, 15>(tile, (uint32_t)(dbase / 8), o[ht], inv, out0 + (size_t)16 * ht * D,
+        store_head_tile<DT, DPV, ROW_BYTES, 15, STREAM>(tile, (uint32_t)(dbase / 8), o[ht], inv, out0 + (size_t)16 * ht * D,
                                                 D, lane);
       }
     };
@@ -1623,12 +1636,13 @@ static SparseArgs make_args(const SparseMlaParams* p, const void* q, const void*
   a.parts = split.parts;
   a.split_from = (int32_t)split.split_from;
   a.ring = p->ring != 0 ? p->ring : (kv_cache_bytes(p) > INFINITY_CACHE_BYTES ? 4 : 3);
-  // Non-temporal KV row loads in the one-item kernel when requests have at
-  // most 16 query tokens on average (decode and multi-token decode: B64 x 6
-  // 62.7 -> 59.8 µs, 85 keys 72.4 -> 69.3 µs). Many tokens of one request
-  // share its rows through the L2, which these loads give up: one request of
-  // 500 tokens measured 58.0 -> 63.4 µs with them (and the persistent prefill
-  // kernel 43% slower).
+  // Non-temporal KV row loads (one-item kernel; and Q and O accesses in the
+  // persistent kernel) when requests have at most 16 query tokens on average
+  // (decode and multi-token decode: B64 x 6 62.7 -> 59.8 µs, 85 keys 72.4 ->
+  // 69.3 µs, B128 x 6 on the persistent kernel 113.2 -> 104.4 µs). Many tokens
+  // of one request share its rows through the L2, which these loads give up:
+  // one request of 500 tokens measured 58.0 -> 63.4 µs with them (and the
+  // persistent prefill kernel 43% slower).
   a.stream_kv = (int64_t)p->T <= 16 * (int64_t)p->B ? 1 : 0;
   a.scale = p->scale;
   return a;
@@ -1697,6 +1711,21 @@ static int launch_persistent(const SparseArgs& a, int ring, hipStream_t stream) 
   static const int cus = device_cus();
   const int64_t items = (int64_t)a.T * (a.H / a.BM);
   const unsigned grid = (unsigned)std::min<int64_t>(cus, items);
+  // Calls of few query tokens per request (a.stream_kv) take the form with
+  // non-temporal KV, Q and O accesses at D = 512 (decode B128 x 6 113.2 ->
+  // 104.4 µs); prefill keeps ordinary ones (non-temporal KV loads made it 43%
+  // slower: consecutive tokens share rows through the L2).
+  if constexpr (D == 512) {
+    if (a.stream_kv) {
+      if (ring == 4)
+        hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4, CLAMP, true>), dim3(grid),
+                           dim3((NQ + NP) * 64), 5 * lds, stream, a);
+      else
+        hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 3, CLAMP, true>), dim3(grid),
+                           dim3((NQ + NP) * 64), 4 * lds, stream, a);
+      return (int)hipGetLastError();
+    }
+  }
   if (ring == 4)
     hipLaunchKernelGGL((sparse_mla_persistent_kernel<DT, D, NQ, NP, 4, CLAMP>), dim3(grid), dim3((NQ + NP) * 64), 5 * lds,
                        stream, a);

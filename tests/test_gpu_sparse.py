@@ -231,6 +231,48 @@ def test_validation_cases_on_the_persistent_stream(device, case, variant, ring):
     assert_lse(lse[torch.as_tensor(tokens, device=device)], sr.oracle_lse(data, policy, tokens))
 
 
+@pytest.mark.parametrize("ring", [3, 4])
+@pytest.mark.parametrize("variant", ["bf16-d512-bm64-r2", "bf16-d512-bm32-r2"])
+@pytest.mark.parametrize("case", ["mixed", "ragged"])
+def test_persistent_stream_with_few_tokens_per_request(device, case, variant, ring):
+    """B40 x T560 (14 query tokens per request on average): more than two work
+    items per CU, so the plan path runs the persistent kernel, and at most 16
+    tokens per request, so at D = 512 it takes its form with non-temporal KV,
+    Q and O accesses (the batched-decode form). Its output and softmax_lse must
+    be bit-identical to the one-item kernel's, its plan must equal the oracle's
+    selection, and a sample must match the oracle; both KV rings, one and two
+    head tiles per token."""
+    from ascendflow_amd.sparse_attention import sparse_mla
+
+    print(f"\n[sparse] persistent few-token case={case} variant={variant} ring={ring}", flush=True)
+    policy = sr.default_policy(B=40, T=560, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
+    data = sr.inputs(policy, case)
+    tensors = to_device(data, policy, device)
+    t = policy["T"]
+    debug = torch.full((t, policy["S"], 2), -7, dtype=torch.int32, device=device)
+    lse_one = torch.full((t, policy["H"]), float("nan"), dtype=torch.float32, device=device)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), debug_rows=debug, softmax_lse=lse_one)
+    torch.cuda.synchronize()
+    one_item = tensors["attention_out"].clone()
+    tensors["attention_out"].fill_(float("nan"))
+    lse = torch.full_like(lse_one, float("nan"))
+    workspace = workspace_for(policy, device, parts=1)
+    sparse_mla(*call_args(tensors), **call_kwargs(policy), parts=1, softmax_lse=lse, workspace=workspace, ring=ring)
+    torch.cuda.synchronize()
+    assert guard_intact(tensors), "kernel wrote past attention_out"
+    every = list(range(t))
+    assert_plan_matches(workspace, data, policy, every)
+    np.testing.assert_array_equal(debug.cpu().numpy(), expected_rows(data, policy, every))
+    assert torch.equal(one_item, tensors["attention_out"]), "persistent stream differs from the one-item kernel"
+    assert torch.equal(lse_one, lse), "persistent softmax_lse differs from the one-item kernel"
+    counts = (debug[..., 0] >= 0).sum(dim=1).cpu().numpy()
+    rng = np.random.default_rng(5)
+    tokens = sorted({0, 1, t - 1, *np.flatnonzero(counts <= 1)[:6].tolist(), *rng.choice(t, 24, replace=False).tolist()})
+    out = tensors["attention_out"].float().cpu().numpy()
+    assert_close(out[tokens], sr.oracle_fp32(data, policy, tokens), policy["DTYPE"])
+    assert_lse(lse[torch.as_tensor(tokens, device=device)], sr.oracle_lse(data, policy, tokens))
+
+
 @pytest.mark.parametrize("shape,ring", [("b8-t544", 3), ("b8-t544", 4), ("b4-t16", None)])
 def test_plan_then_planned_attention_equals_the_call(device, shape, ring):
     """launch_sparse_mla_plan followed by launch_sparse_mla_planned (the
