@@ -14,7 +14,8 @@
 // One workgroup per token; the selection works on a monotonic 32-bit key of
 // each score. sparse_topk_filter (rows up to 256K positions; 256 threads up
 // to 32K positions, 1024 beyond):
-//   1. sample: four keys per thread, in blocks of 16 consecutive positions
+//   1. sample: four keys per thread (two in the 1024-thread form: 2048
+//      keys), in blocks of 16 consecutive positions
 //      evenly spaced over the row (issued with the request lookup, over the
 //      whole allocated row, and kept when the token's candidates cover at
 //      least half of it; shorter rows are sampled again over their
@@ -48,7 +49,13 @@ namespace afa {
 constexpr int TK_BINS = 2048;  // widest digit: 11 bits
 constexpr int TK_UNROLL = 4;    // 4-position groups in flight per thread in a streaming pass
 constexpr int TK_FILTER_ROUNDS = 4;  // filter passes before the whole-row selection
-constexpr int TK_SAMPLES = 4;        // sample keys per thread for the threshold estimate
+// Sample keys per thread for the threshold estimate: 4 x 256 = 1024 keys in
+// the 256-thread form, whose buffer of 2 TOPK entries needs the closer
+// estimate; 2 x 1024 = 2048 in the 1024-thread form (4096 entries), where
+// the sample's histogram atomics, crowded into the few bins that the leading
+// digit of similar scores falls into, had made the estimate a tenth of the
+// kernel (decode 38.4 -> 36.3 µs against 4096 keys).
+template <int THREADS> constexpr int TK_SAMPLES = THREADS <= 256 ? 4 : 2;
 constexpr int TK_WIDE_CAP = 4096;    // filter buffer entries of the 1024-thread form
 constexpr int64_t TK_FILTER_MAX_C = 262144;  // two LDS bitmaps of C bits each
 // Word 3 of a raw buffer resource on gfx9-family GPUs (32-bit data format,
@@ -368,32 +375,33 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
   // 1. Sample: S keys in blocks of 16 consecutive positions (64 bytes), the
   // S / 16 blocks evenly spaced over a range of n positions (block b from
   // position floor(b n / (S / 16))), so the sample touches few cache lines;
-  // thread t holds samples 4t .. 4t + 3. The first sample, S = min(TK_SAMPLES
-  // THREADS, C) over the whole allocated row (n = C), goes out before the
-  // request lookup; its keys at positions past the token's candidates are
+  // thread t holds samples SPT t .. SPT t + SPT - 1. The first sample, S =
+  // min(SPT THREADS, C) over the whole allocated row (n = C), goes out before
+  // the request lookup; its keys at positions past the token's candidates are
   // left out, and when the candidates cover less than half of the row (or C
-  // < TK_SAMPLES THREADS) the row is sampled again over them (n = cand,
-  // S = min(TK_SAMPLES THREADS, cand), a row shorter than that whole).
-  // A sample shorter than TK_SAMPLES THREADS is the whole range (block
+  // < SPT THREADS) the row is sampled again over them (n = cand,
+  // S = min(SPT THREADS, cand), a row shorter than that whole).
+  // A sample shorter than SPT THREADS is the whole range (block
   // positions i); otherwise it has SAMPLE_BLOCKS blocks, a power of two, so
   // floor(b n / SAMPLE_BLOCKS) is a shift. The loads are unconditional
   // (positions past the buffer's range read 0) and their words are turned
   // into keys only where they are used, so that the four go out together
   // with the request lookup's and share its round trip.
-  constexpr int SAMPLE_BLOCKS = TK_SAMPLES * THREADS / 16;
+  constexpr int SPT = TK_SAMPLES<THREADS>;
+  constexpr int SAMPLE_BLOCKS = SPT * THREADS / 16;
   constexpr int SAMPLE_SHIFT = __builtin_ctz(SAMPLE_BLOCKS);
   static_assert((SAMPLE_BLOCKS & (SAMPLE_BLOCKS - 1)) == 0, "sample blocks must be a power of two");
   auto sample_position = [&](int i, int64_t n, int s) {
-    return s < TK_SAMPLES * THREADS ? i : (int)(((int64_t)(i >> 4) * n) >> SAMPLE_SHIFT) + (i & 15);
+    return s < SPT * THREADS ? i : (int)(((int64_t)(i >> 4) * n) >> SAMPLE_SHIFT) + (i & 15);
   };
-  const int samples_c = (int)min<int64_t>(TK_SAMPLES * THREADS, a.C);
+  const int samples_c = (int)min<int64_t>(SPT * THREADS, a.C);
   const __amdgpu_buffer_rsrc_t rsrc_row = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(a.scores + (size_t)token * a.C), (short)0, (int)(a.C * 4), BUFFER_WORD3);
-  uint32_t sample[TK_SAMPLES];  // the score words, then their keys
-  int sample_pos[TK_SAMPLES];
+  uint32_t sample[SPT];  // the score words, then their keys
+  int sample_pos[SPT];
 #pragma unroll
-  for (int j = 0; j < TK_SAMPLES; ++j) {
-    sample_pos[j] = sample_position(tid * TK_SAMPLES + j, a.C, samples_c);
+  for (int j = 0; j < SPT; ++j) {
+    sample_pos[j] = sample_position(tid * SPT + j, a.C, samples_c);
     sample[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc_row, sample_pos[j] * 4, 0, 0);
   }
   // Request lookup. B <= THREADS: one round trip, thread b loading request
@@ -433,13 +441,13 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
   uint32_t* equal_bits = bitmaps + words;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(a.scores + (size_t)token * a.C), (short)0, cand * 4, BUFFER_WORD3);
-  const bool whole_row_sample = samples_c == TK_SAMPLES * THREADS && 2 * (int64_t)cand >= a.C;  // uniform
+  const bool whole_row_sample = samples_c == SPT * THREADS && 2 * (int64_t)cand >= a.C;  // uniform
   int samples = 0;           // keys in the sample
   uint32_t sample_mask = 0;  // bit j: sample[j] is one of them
   if (whole_row_sample) {
     int mine = 0;
 #pragma unroll
-    for (int j = 0; j < TK_SAMPLES; ++j) {
+    for (int j = 0; j < SPT; ++j) {
       sample[j] = score_key(__uint_as_float(sample[j]));  // every sample is in [0, C) here
       const bool in_row = sample_pos[j] < cand;
       sample_mask |= in_row ? 1u << j : 0u;
@@ -448,13 +456,13 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
     mine = __builtin_amdgcn_readlane(wave_inclusive_scan(mine), 63);
     if (lane == 0) scan_scratch[WAVES + wave] = mine;  // summed after the barrier below
   } else {
-    samples = min(TK_SAMPLES * THREADS, cand);
+    samples = min(SPT * THREADS, cand);
 #pragma unroll
-    for (int j = 0; j < TK_SAMPLES; ++j)
-      sample[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, sample_position(tid * TK_SAMPLES + j, cand, samples) * 4, 0, 0);
+    for (int j = 0; j < SPT; ++j)
+      sample[j] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, sample_position(tid * SPT + j, cand, samples) * 4, 0, 0);
 #pragma unroll
-    for (int j = 0; j < TK_SAMPLES; ++j) {
-      const int i = tid * TK_SAMPLES + j;
+    for (int j = 0; j < SPT; ++j) {
+      const int i = tid * SPT + j;
       sample[j] = i < samples ? score_key(__uint_as_float(sample[j])) : 0u;
       sample_mask |= i < samples ? 1u << j : 0u;
     }
@@ -489,7 +497,7 @@ __global__ __launch_bounds__(THREADS, 8) void sparse_topk_filter(TopkArgs a) {
     const uint32_t estimate = radix_select<THREADS, COMPACT, 2>(
         [&](auto f) {
 #pragma unroll
-          for (int j = 0; j < TK_SAMPLES; ++j)
+          for (int j = 0; j < SPT; ++j)
             if ((sample_mask >> j) & 1u) f(sample[j]);
         },
         rank, radix, parity, &unused);  // ends with a barrier: every read of `reached` is done

@@ -164,20 +164,22 @@ def test_random_scores_at_full_size(device, name):
 @pytest.mark.parametrize("case", ["estimate-holds", "estimate-refiltered", "estimate-too-high", "buffer-overflow"])
 def test_estimate_fallbacks(device, c, case):
     """The filter kernel (256 threads up to 32K positions, 1024 beyond)
-    estimates the threshold from S = 4 x threads sampled keys (the whole row
-    when shorter: sample i in block i // 16 of 16 consecutive positions, block
-    b starting at floor(b c / (S / 16))) and selects from the keys that reach it.
+    estimates the threshold from S sampled keys, 4 per thread of 256 (1024)
+    or 2 per thread of 1024 (2048); the whole row when shorter: sample i in
+    block i // 16 of 16 consecutive positions, block b starting at
+    floor(b c / (S / 16)), and selects from the keys that reach it.
     When fewer than TOPK reach it, or more than its LDS buffer holds (2 TOPK
     entries within [1024, 8192] up to 32K positions, 4096 beyond), it filters again at another sample rank (binary search,
     up to four passes), then selects from the whole row. Large scores on a
     32nd of the sampled positions need further passes; on all of them the
     estimate stays too high once TOPK exceeds the sample; a TOPK of 9000
     overflows the buffer. Every outcome must select the same."""
-    samples = min(4 * (256 if c <= 32768 else 1024), c)
+    full = 4 * 256 if c <= 32768 else 2 * 1024
+    samples = min(full, c)
     topk = {"estimate-holds": samples // 4 - 12, "estimate-refiltered": samples // 32 + 40,
             "estimate-too-high": samples + 88, "buffer-overflow": 9000}[case]
     i = np.arange(samples)
-    sampled = i if samples < 4 * (256 if c <= 32768 else 1024) else (i // 16) * c // (samples // 16) + i % 16
+    sampled = i if samples < full else (i // 16) * c // (samples // 16) + i % 16
     scores = np.random.default_rng(c + topk).normal(size=(2, c)).astype(np.float32)
     scores[0, sampled[::32] if case == "estimate-refiltered" else sampled] = 10.0
     cu = np.array([0, 2], np.int32)
