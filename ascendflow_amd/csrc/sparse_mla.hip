@@ -447,6 +447,8 @@ constexpr int LOOK_QK = 5;  // KV fragment lookahead (k-steps) of a score wave
 // fetch (8 rows each) and the score waves, whose step is the longer one, only
 // wait at the barrier (decode B64 x 6 ~2% faster than every wave fetching 4
 // rows); other shapes spread the fetch over every wave.
+// STREAM_KV: KV row loads are non-temporal as well (Q and O always are), for
+// calls whose requests have few query tokens.
 template <int DT, int D, int NQ, int NP, int NS, bool STREAM_KV = false>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
@@ -877,6 +879,10 @@ struct Cursor {
 //    sink's e^(sink - m)), its output accumulators are cleared on its first PV
 //    step, and its denominator travels through LDS slot item & 1.
 // The first item's Q goes through LDS as in sparse_mla_kernel.
+// STREAM: KV row loads, next-item Q loads and O stores are non-temporal, for
+// calls whose requests have few query tokens (batched decode: rows shared by
+// few tokens); prefill keeps ordinary accesses, its consecutive tokens
+// sharing rows through the L2.
 template <int DT, int D, int NQ, int NP, int NS, bool CLAMP, bool STREAM = false>
 __global__ __launch_bounds__((NQ + NP) * 64) void sparse_mla_persistent_kernel(SparseArgs a) {
   typedef typename B16<DT>::scalar scalar;
