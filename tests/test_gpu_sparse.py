@@ -273,19 +273,21 @@ def test_persistent_stream_with_few_tokens_per_request(device, case, variant, ri
     assert_lse(lse[torch.as_tensor(tokens, device=device)], sr.oracle_lse(data, policy, tokens))
 
 
-@pytest.mark.parametrize("shape,ring", [("b8-t544", 3), ("b8-t544", 4), ("b4-t16", None)])
+@pytest.mark.parametrize("shape,ring", [("b8-t544", 3), ("b8-t544", 4), ("b40-t560", 3), ("b40-t560", 4), ("b4-t16", None)])
 def test_plan_then_planned_attention_equals_the_call(device, shape, ring):
     """launch_sparse_mla_plan followed by launch_sparse_mla_planned (the
     persistent kernel alone over that plan) gives sparse_mla's output and
     softmax_lse bit for bit: at T544 (where sparse_mla itself takes the plan
-    path; each KV ring) and at T16 (where it runs the one-item kernel, whose
-    output the persistent kernel matches bit for bit when no key is split:
-    parts=1, and the planned call still runs the persistent kernel)."""
+    path; each KV ring), at B40 x T560 (14 tokens per request: the plan path
+    with the persistent kernel's non-temporal form) and at T16 (where it runs
+    the one-item kernel, whose output the persistent kernel matches bit for
+    bit when no key is split: parts=1, and the planned call still runs the
+    persistent kernel)."""
     from ascendflow_amd.sparse_attention import sparse_mla, sparse_mla_planned
     from ascendflow_amd.sparse_attention.probe import sparse_mla_plan
 
     print(f"\n[sparse] plan + planned {shape} ring={ring}", flush=True)
-    b, t = (8, 544) if shape == "b8-t544" else (4, 16)
+    b, t = {"b8-t544": (8, 544), "b40-t560": (40, 560), "b4-t16": (4, 16)}[shape]
     policy = sr.default_policy(B=b, T=t, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160)
     data = sr.inputs(policy, "mixed")
     tensors = to_device(data, policy, device)
