@@ -233,19 +233,21 @@ def test_validation_cases_on_the_persistent_stream(device, case, variant, ring):
 
 @pytest.mark.parametrize("ring", [3, 4])
 @pytest.mark.parametrize("variant", ["bf16-d512-bm64-r2", "bf16-d512-bm32-r2"])
-@pytest.mark.parametrize("case", ["mixed", "ragged"])
+@pytest.mark.parametrize("case", sr.CASES)
 def test_persistent_stream_with_few_tokens_per_request(device, case, variant, ring):
     """B40 x T560 (14 query tokens per request on average): more than two work
     items per CU, so the plan path runs the persistent kernel, and at most 16
     tokens per request, so at D = 512 it takes its form with non-temporal KV,
-    Q and O accesses (the batched-decode form). Its output and softmax_lse must
-    be bit-identical to the one-item kernel's, its plan must equal the oracle's
-    selection, and a sample must match the oracle; both KV rings, one and two
-    head tiles per token."""
+    Q and O accesses (the batched-decode form). On each of the eight
+    validation cases its output and softmax_lse must be bit-identical to the
+    one-item kernel's, its plan must equal the oracle's selection, and a
+    sample must match the oracle (all zero for empty selections); both KV
+    rings, one and two head tiles per token."""
     from ascendflow_amd.sparse_attention import sparse_mla
 
     print(f"\n[sparse] persistent few-token case={case} variant={variant} ring={ring}", flush=True)
     policy = sr.default_policy(B=40, T=560, MAX_SEQ=4096, ORI_BLOCKS=160, CMP_BLOCKS=160, **VARIANTS[variant])
+    policy["SCALE"] = policy["D"] ** -0.5
     data = sr.inputs(policy, case)
     tensors = to_device(data, policy, device)
     t = policy["T"]
@@ -269,6 +271,8 @@ def test_persistent_stream_with_few_tokens_per_request(device, case, variant, ri
     rng = np.random.default_rng(5)
     tokens = sorted({0, 1, t - 1, *np.flatnonzero(counts <= 1)[:6].tolist(), *rng.choice(t, 24, replace=False).tolist()})
     out = tensors["attention_out"].float().cpu().numpy()
+    if case == "empty":
+        assert np.all(out == 0)
     assert_close(out[tokens], sr.oracle_fp32(data, policy, tokens), policy["DTYPE"])
     assert_lse(lse[torch.as_tensor(tokens, device=device)], sr.oracle_lse(data, policy, tokens))
 
